@@ -1,0 +1,281 @@
+"""Algebraic FlashAttention on MI355X: the call surface of src/kernels/pallas_afa.py.
+
+Same names, argument meanings, defaults and ValueError checks as the reference module
+(tasmaikeni13/algebraic-intelligence, src/kernels/pallas_afa.py), on torch tensors that live on
+a HIP device.  Every function launches the gfx950 kernels of libafa_hip.so through the C ABI in
+include/afa.h; there is no CPU implementation behind them.
+
+Beyond the reference signatures, the forward entry points take ``rotary_params`` (a
+CayleyRotary or a (c, s) pair of (>= L, D/2) tables): q and k are then rotated inside the
+kernel at tile load, which fuses the model's ``_rotate_tensor`` calls (src/model.py:262-264).
+
+``block_q`` / ``block_k`` are validated exactly as the reference does, but they do not change
+the computation: the kernels pick their own tiles, and the additive accumulation makes the
+result independent of the tiling (src/kernels/pallas_afa.py tests, test_additive_tile_associativity).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "pallas_afa_forward", "tiled_afa_forward", "exact_afa_reference", "exact_afa_with_denominator",
+    "tiled_afa_backward", "pallas_afa", "algebraic_flash_attention",
+]
+
+
+def _finite_nonneg(x) -> bool:
+    return 0.0 <= float(x) < float("inf")
+
+
+def _rotary_tables(rotary_params, q: torch.Tensor):
+    """(c, s) device tables in the kernel's table type: fp32, or fp64 for fp64 inputs."""
+    if rotary_params is None:
+        return None, None, 0
+    if isinstance(rotary_params, (tuple, list)) and len(rotary_params) >= 2:
+        c, s = rotary_params[0], rotary_params[1]
+    elif hasattr(rotary_params, "c") and hasattr(rotary_params, "s"):
+        c, s = rotary_params.c, rotary_params.s
+    else:
+        raise TypeError(f"Unsupported rotary parameters type: {type(rotary_params)}")
+    tdt = torch.float64 if q.dtype == torch.float64 else torch.float32
+    D = q.shape[-1]
+    c = torch.as_tensor(c, device=q.device).to(tdt).reshape(-1, D // 2).contiguous()
+    s = torch.as_tensor(s, device=q.device).to(tdt).reshape(-1, D // 2).contiguous()
+    if c.shape != s.shape:
+        raise ValueError(f"rotary tables must match, got {tuple(c.shape)} and {tuple(s.shape)}")
+    return c, s, c.shape[0]
+
+
+def _strides(*ts):
+    """12 element strides (b, h, l per tensor); head_dim must be contiguous."""
+    out = []
+    for t in ts:
+        out.extend(t.stride()[:3])
+    return (ctypes.c_int64 * 12)(*out)
+
+
+def _prep(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _launch_fwd(q, k, v, sink_omega, causal, valid_seq_len, rotary_params, flags,
+                want_denominator):
+    dev = _lib.require_device(q, k, v)
+    dt = _lib.dtype_code(q.dtype)
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError(f"q, k and v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    B, H, L, D = q.shape
+    out = torch.empty((B, H, L, D), dtype=q.dtype, device=dev)
+    den = torch.empty((B, H, L, 1), dtype=_lib.accum_dtype(q.dtype), device=dev) if want_denominator else None
+    c, s, rot_len = _rotary_tables(rotary_params, q)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().afa_fwd(
+            dt, B, H, L, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _strides(q, k, v, out),
+            _lib.ptr(out), _lib.ptr(den), _lib.ptr(c), _lib.ptr(s), rot_len, float(sink_omega),
+            int(bool(causal)), 0 if valid_seq_len is None else int(valid_seq_len), flags,
+            _lib.stream_ptr(dev))
+    _lib.check(rc, "afa_fwd")
+    return out, den
+
+
+def pallas_afa_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    sink_omega: float = 0.5,
+    causal: bool = False,
+    block_q: int = 128,
+    block_k: int = 128,
+    valid_seq_len: Optional[int] = None,
+    interpret: Optional[bool] = None,
+    return_denominator: bool = False,
+    *,
+    rotary_params=None,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Fused AFA forward (src/kernels/pallas_afa.py:154-264).
+
+    Returns out (q.dtype) or (out, d) with d = sum_j rho(s_ij)^8 + sink_omega of shape
+    (B, H, L, 1) in fp32 (fp64 for fp64 inputs).  ``interpret`` is accepted for signature
+    compatibility; the reference uses it to pick the Pallas interpreter off-TPU, and here the
+    HIP kernel runs either way.
+    """
+    del interpret
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must all have shape (batch, heads, sequence, dimension)")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q, k, and v shapes must match, got {tuple(q.shape)}, {tuple(k.shape)}, and {tuple(v.shape)}")
+    if not _finite_nonneg(sink_omega):
+        raise ValueError("sink_omega must be finite and nonnegative")
+    if block_q <= 0 or block_k <= 0:
+        raise ValueError("block_q and block_k must be positive")
+    batch_size, num_heads, seq_len, head_dim = q.shape
+    if head_dim <= 0:
+        raise ValueError("head dimension must be positive")
+    if head_dim > 128 and head_dim % 128 != 0:
+        raise ValueError("head dimensions above 128 must be divisible by 128")
+    if seq_len % block_q != 0 or seq_len % block_k != 0:
+        raise ValueError(
+            f"seq_len ({seq_len}) must be divisible by block_q ({block_q}) and block_k ({block_k})"
+        )
+    if valid_seq_len is not None and not 0 < valid_seq_len <= seq_len:
+        raise ValueError("valid_seq_len must be in [1, seq_len]")
+    out, den = _launch_fwd(q, k, v, sink_omega, causal, valid_seq_len, rotary_params, 0,
+                           return_denominator)
+    return (out, den) if return_denominator else out
+
+
+def tiled_afa_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    sink_omega: float = 0.5,
+    causal: bool = False,
+    block_q: int = 128,
+    block_k: int = 128,
+    valid_seq_len: Optional[int] = None,
+    return_denominator: bool = False,
+    *,
+    rotary_params=None,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Tiled additive AFA (src/kernels/pallas_afa.py:330-406): the same function as
+    pallas_afa_forward, with the reference's own argument checks."""
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, and v must have the same four-dimensional shape")
+    if not _finite_nonneg(sink_omega):
+        raise ValueError("sink_omega must be finite and nonnegative")
+    if block_q <= 0 or block_k <= 0:
+        raise ValueError("block_q and block_k must be positive")
+    seq_len = q.shape[2]
+    if seq_len % block_q != 0 or seq_len % block_k != 0:
+        raise ValueError("sequence length must be divisible by both tile dimensions")
+    if valid_seq_len is not None and not 0 < valid_seq_len <= seq_len:
+        raise ValueError("valid_seq_len must be in [1, seq_len]")
+    out, den = _launch_fwd(q, k, v, sink_omega, causal, valid_seq_len, rotary_params, 0,
+                           return_denominator)
+    return (out, den) if return_denominator else out
+
+
+def exact_afa_reference(q, k, v, sink_omega: float = 0.5, causal: bool = False) -> torch.Tensor:
+    """Untiled reference contract (src/kernels/pallas_afa.py:267-297): q * scale rounded to
+    q.dtype before the dot, row sum of P cast to v.dtype, out = O * (1 / (D + sink)).
+
+    For bf16/fp16 inputs the reference additionally evaluates S and rho^8 in the input dtype;
+    here they are evaluated in fp32.
+    """
+    return exact_afa_with_denominator(q, k, v, sink_omega, causal)[0]
+
+
+def exact_afa_with_denominator(q, k, v, sink_omega: float = 0.5, causal: bool = False):
+    """(out, d_total) of the untiled contract (src/kernels/pallas_afa.py:300-327); d_total is
+    returned in v.dtype, as the reference sums P after casting it to v.dtype."""
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, and v must have the same four-dimensional shape")
+    if not _finite_nonneg(sink_omega):
+        raise ValueError("sink_omega must be finite and nonnegative")
+    out, den = _launch_fwd(q, k, v, sink_omega, causal, None, None, _lib.FLAG_EXACT_REF, True)
+    return out, den.to(v.dtype)
+
+
+def tiled_afa_backward(
+    q, k, v, out, d_total, g_out, sink_omega: float = 0.5, causal: bool = False,
+    block_q: int = 128, block_k: int = 128, valid_seq_len: Optional[int] = None, *,
+    rotary_params=None,
+):
+    """Analytical AFA backward (src/kernels/pallas_afa.py:409-522): (dq, dk, dv) in the input
+    dtypes.  With ``rotary_params`` the forward rotated q and k in-kernel and dq, dk are with
+    respect to the unrotated inputs."""
+    del block_q, block_k
+    dev = _lib.require_device(q, k, v, out, d_total, g_out)
+    dt = _lib.dtype_code(q.dtype)
+    B, H, L, D = q.shape
+    q, k, v, out, g_out = (t.contiguous() for t in (q, k, v, out, g_out))
+    d_total = d_total.to(_lib.accum_dtype(q.dtype)).contiguous()
+    dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
+    c, s, rot_len = _rotary_tables(rotary_params, q)
+    ws_bytes = _lib.lib().afa_bwd_workspace_size(dt, B, H, L, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().afa_bwd(
+            dt, B, H, L, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(d_total),
+            _lib.ptr(g_out), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(c), _lib.ptr(s),
+            rot_len, float(sink_omega), int(bool(causal)),
+            0 if valid_seq_len is None else int(valid_seq_len), 0, _lib.ptr(ws), ws_bytes,
+            _lib.stream_ptr(dev))
+    _lib.check(rc, "afa_bwd")
+    return dq, dk, dv
+
+
+class _PallasAFA(torch.autograd.Function):
+    """Custom VJP of pallas_afa (src/kernels/pallas_afa.py:532-615): the forward keeps
+    (q, k, v, out, d_total) and the backward is the analytical tiled_afa_backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, sink_omega, causal, valid_seq_len, rotary_params):
+        out, den = _launch_fwd(q, k, v, sink_omega, causal, valid_seq_len, rotary_params, 0, True)
+        ctx.save_for_backward(q, k, v, out, den)
+        ctx.cfg = (sink_omega, causal, valid_seq_len, rotary_params)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        q, k, v, out, den = ctx.saved_tensors
+        sink_omega, causal, valid_seq_len, rotary_params = ctx.cfg
+        dq, dk, dv = tiled_afa_backward(q, k, v, out, den, g, sink_omega, causal,
+                                        valid_seq_len=valid_seq_len, rotary_params=rotary_params)
+        return dq, dk, dv, None, None, None, None
+
+
+def pallas_afa(
+    q, k, v, sink_omega: float = 0.5, causal: bool = False, block_q: int = 128,
+    block_k: int = 128, valid_seq_len: Optional[int] = None, *, rotary_params=None,
+) -> torch.Tensor:
+    """Differentiable fused AFA (src/kernels/pallas_afa.py:579-615)."""
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, and v must have the same four-dimensional shape")
+    if not _finite_nonneg(sink_omega):
+        raise ValueError("sink_omega must be finite and nonnegative")
+    if block_q <= 0 or block_k <= 0:
+        raise ValueError("block_q and block_k must be positive")
+    seq_len = q.shape[2]
+    if seq_len % block_q != 0 or seq_len % block_k != 0:
+        raise ValueError(
+            f"seq_len ({seq_len}) must be divisible by block_q ({block_q}) and block_k ({block_k})"
+        )
+    if valid_seq_len is not None and not 0 < valid_seq_len <= seq_len:
+        raise ValueError("valid_seq_len must be in [1, seq_len]")
+    return _PallasAFA.apply(q, k, v, float(sink_omega), bool(causal), valid_seq_len, rotary_params)
+
+
+def algebraic_flash_attention(
+    q, k, v, sink_omega: float = 0.5, causal: bool = False, block_q: int = 128,
+    block_k: int = 128, *, rotary_params=None,
+) -> torch.Tensor:
+    """Unified entry point for any sequence length (src/kernels/pallas_afa.py:695-739).
+
+    The reference pads L up to lcm(block_q, block_k), masks the padded keys with
+    valid_seq_len and slices the padded queries off.  The HIP kernels take any L directly and
+    give the same values without the padded copies: padded keys carry zero weight and padded
+    queries are never stored.
+    """
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, and v must have the same four-dimensional shape")
+    if block_q <= 0 or block_k <= 0:
+        raise ValueError("block_q and block_k must be positive")
+    if not _finite_nonneg(sink_omega):
+        raise ValueError("sink_omega must be finite and nonnegative")
+    if q.shape[-1] > 128 and q.shape[-1] % 128 != 0:
+        raise ValueError("head dimensions above 128 must be divisible by 128")
+    return _PallasAFA.apply(q, k, v, float(sink_omega), bool(causal), None, rotary_params)
+
+
+def afa_flops(batch: int, heads: int, seq_len: int, head_dim: int, causal: bool) -> int:
+    """Algorithmic FLOPs of one forward: 4 B H D N_pairs (QK^T + PV over unmasked pairs),
+    N_pairs = L^2 or L(L+1)/2 (scripts/run_phase6_tpu.py:236 for the non-causal form)."""
+    pairs = seq_len * (seq_len + 1) // 2 if causal else seq_len * seq_len
+    return 4 * batch * heads * head_dim * pairs

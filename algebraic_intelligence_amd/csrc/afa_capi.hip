@@ -1,0 +1,257 @@
+// C ABI of libafa_hip.so (declared in include/afa.h): argument validation mirroring the
+// reference's ValueError checks, path selection, and kernel dispatch.
+#include <cmath>
+#include <cstdint>
+
+#include "../../include/afa.h"
+#include "afa_launch.h"
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int hip_status(hipError_t e) {
+  if (e == hipSuccess) return AFA_OK;
+  g_last_hip_error = (int)e;
+  return AFA_ERR_HIP;
+}
+
+bool finite_nonneg(double x) { return x >= 0.0 && x < INFINITY; }  // NaN fails both
+bool valid_dtype(int dt) { return dt == AFA_F32 || dt == AFA_BF16 || dt == AFA_F16 || dt == AFA_F64; }
+size_t elem_size(int dt) { return dt == AFA_F64 ? 8 : dt == AFA_F32 ? 4 : 2; }
+size_t acc_size(int dt) { return dt == AFA_F64 ? 8 : 4; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Cancellation error of the branch-free rho for s < 0 is at most 6e-9 per weight (absolute);
+// over n keys the relative error of out is below n * 6e-9 / sink_omega.  The fast form is
+// used only where that bound stays below 1e-3 (the bf16 rounding of P alone is 2e-3), and
+// never for fp32/fp64 inputs.
+bool fast_rho_ok(double sink_omega, int64_t seq_len) {
+  return sink_omega > 0.0 && (double)seq_len * 6e-9 / sink_omega < 1e-3;
+}
+
+struct Strides {
+  int64_t v[12];
+};
+
+Strides resolve_strides(const int64_t* s, int64_t H, int64_t L, int64_t D) {
+  Strides r;
+  if (s == nullptr) {
+    for (int t = 0; t < 4; ++t) {
+      r.v[3 * t + 0] = H * L * D;
+      r.v[3 * t + 1] = L * D;
+      r.v[3 * t + 2] = D;
+    }
+  } else {
+    for (int i = 0; i < 12; ++i) r.v[i] = s[i];
+  }
+  return r;
+}
+
+int check_rotary(const void* rc, const void* rs, int64_t rot_len, int64_t L, int64_t D) {
+  if ((rc == nullptr) != (rs == nullptr)) return AFA_ERR_ROTARY;
+  if (rc != nullptr && (rot_len < L || D % 2 != 0)) return AFA_ERR_ROTARY;
+  return AFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* afa_status_string(int status) {
+  switch (status) {
+    case AFA_OK: return "ok";
+    case AFA_ERR_NULL: return "a required pointer is NULL";
+    case AFA_ERR_DTYPE: return "unsupported dtype";
+    case AFA_ERR_SHAPE: return "q, k, and v must all have shape (batch, heads, sequence, dimension) with positive sizes";
+    case AFA_ERR_HEAD_DIM: return "head dimensions above 128 must be divisible by 128";
+    case AFA_ERR_SINK: return "sink_omega must be finite and nonnegative";
+    case AFA_ERR_VALID_LEN: return "valid_seq_len must be in [1, seq_len]";
+    case AFA_ERR_EPS: return "eps must be finite and positive";
+    case AFA_ERR_ROTARY: return "rotary tables must both be given, cover seq_len rows and need an even head dimension";
+    case AFA_ERR_ALIGN: return "stride or pointer alignment not supported";
+    case AFA_ERR_WORKSPACE: return "workspace too small";
+    case AFA_ERR_UNSUPPORTED: return "combination not supported by this build";
+    case AFA_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+int afa_last_hip_error(void) { return g_last_hip_error; }
+
+int afa_version(void) { return 1; }
+
+int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+            const void* q, const void* k, const void* v, const int64_t* strides, void* out,
+            void* denom, const void* rot_cos, const void* rot_sin, int64_t rot_len,
+            double sink_omega, int causal, int64_t valid_len, unsigned flags, void* stream) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return AFA_ERR_NULL;
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return AFA_ERR_SHAPE;
+  if (batch * heads > INT32_MAX / 4 || seq_len > (INT32_MAX >> 2)) return AFA_ERR_SHAPE;
+  if (head_dim > 128 && head_dim % 128 != 0) return AFA_ERR_HEAD_DIM;
+  if (!finite_nonneg(sink_omega)) return AFA_ERR_SINK;
+  if (valid_len < 0 || valid_len > seq_len) return AFA_ERR_VALID_LEN;
+  int rc = check_rotary(rot_cos, rot_sin, rot_len, seq_len, head_dim);
+  if (rc != AFA_OK) return rc;
+  const int vlen = valid_len == 0 ? (int)seq_len : (int)valid_len;
+  const Strides st = resolve_strides(strides, heads, seq_len, head_dim);
+  hipStream_t s = (hipStream_t)stream;
+
+  bool use_mfma = afa::mfma_fwd_supported(dtype, (int)head_dim) && !(flags & AFA_FLAG_GENERIC) &&
+                  !(flags & AFA_FLAG_EXACT_REF);
+  if (use_mfma) {
+    // 16-byte vector loads/stores: 8-element aligned row strides and 16-byte aligned bases.
+    for (int i = 0; i < 12; ++i)
+      if (st.v[i] % 8 != 0) use_mfma = false;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) use_mfma = false;
+    if (rot_cos != nullptr && (!aligned16(rot_cos) || !aligned16(rot_sin))) use_mfma = false;
+  }
+  if (use_mfma) {
+    afa::FwdArgs a;
+    a.q = q; a.k = k; a.v = v; a.out = out; a.denom = (float*)denom;
+    a.rc = (const float*)rot_cos; a.rs = (const float*)rot_sin;
+    a.q_b = st.v[0]; a.q_h = st.v[1]; a.q_l = st.v[2];
+    a.k_b = st.v[3]; a.k_h = st.v[4]; a.k_l = st.v[5];
+    a.v_b = st.v[6]; a.v_h = st.v[7]; a.v_l = st.v[8];
+    a.o_b = st.v[9]; a.o_h = st.v[10]; a.o_l = st.v[11];
+    a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len;
+    a.valid_len = vlen;
+    a.causal = causal ? 1 : 0;
+    const int qpb = afa::mfma_fwd_queries_per_block((int)head_dim);
+    a.nqb = (int)((seq_len + qpb - 1) / qpb);
+    a.omega = (float)sink_omega;
+    a.q_scale = 1.0f;
+    a.w_unscale = 1.0f;
+    const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, vlen);
+    return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
+  }
+  if (head_dim > 256) return AFA_ERR_UNSUPPORTED;
+  afa::GenArgs g = {};
+  g.q = q; g.k = k; g.v = v; g.out = out; g.denom = denom;
+  g.rc = rot_cos; g.rs = rot_sin;
+  g.q_b = st.v[0]; g.q_h = st.v[1]; g.q_l = st.v[2];
+  g.k_b = st.v[3]; g.k_h = st.v[4]; g.k_l = st.v[5];
+  g.v_b = st.v[6]; g.v_h = st.v[7]; g.v_l = st.v[8];
+  g.o_b = st.v[9]; g.o_h = st.v[10]; g.o_l = st.v[11];
+  g.B = (int)batch; g.H = (int)heads; g.L = (int)seq_len; g.D = (int)head_dim;
+  g.valid_len = vlen;
+  g.causal = causal ? 1 : 0;
+  g.exact_ref = (flags & AFA_FLAG_EXACT_REF) ? 1 : 0;
+  g.scale = 1.0 / std::sqrt((double)head_dim);
+  if (dtype != AFA_F64) g.scale = (double)(float)g.scale;
+  g.omega = dtype == AFA_F64 ? sink_omega : (double)(float)sink_omega;
+  return hip_status(afa::generic_fwd_launch(dtype, g, s));
+}
+
+size_t afa_bwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                              int64_t head_dim) {
+  (void)head_dim;
+  if (!valid_dtype(dtype) || batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+  return (size_t)(batch * heads * seq_len) * acc_size(dtype);
+}
+
+int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+            const void* q, const void* k, const void* v, const void* out, const void* denom,
+            const void* g, void* dq, void* dk, void* dv, const void* rot_cos,
+            const void* rot_sin, int64_t rot_len, double sink_omega, int causal,
+            int64_t valid_len, unsigned flags, void* workspace, size_t workspace_bytes,
+            void* stream) {
+  (void)flags;
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (!q || !k || !v || !out || !denom || !g || !dq || !dk || !dv) return AFA_ERR_NULL;
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return AFA_ERR_SHAPE;
+  if (batch * heads * ((seq_len + 31) / 32) > INT32_MAX) return AFA_ERR_SHAPE;
+  if (head_dim > 128 && head_dim % 128 != 0) return AFA_ERR_HEAD_DIM;
+  if (head_dim > 256) return AFA_ERR_UNSUPPORTED;
+  if (!finite_nonneg(sink_omega)) return AFA_ERR_SINK;
+  if (valid_len < 0 || valid_len > seq_len) return AFA_ERR_VALID_LEN;
+  int rc = check_rotary(rot_cos, rot_sin, rot_len, seq_len, head_dim);
+  if (rc != AFA_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t need = afa_bwd_workspace_size(dtype, batch, heads, seq_len, head_dim);
+  void* ws = workspace;
+  bool owned = false;
+  if (ws == nullptr) {
+    hipError_t e = hipMallocAsync(&ws, need, s);
+    if (e != hipSuccess) return hip_status(e);
+    owned = true;
+  } else if (workspace_bytes < need) {
+    return AFA_ERR_WORKSPACE;
+  }
+  afa::GenArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.out_in = out; a.dtot = denom; a.g = g;
+  a.out = dq; a.dk = dk; a.dv = dv; a.e_ws = ws;
+  a.rc = rot_cos; a.rs = rot_sin;
+  a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len; a.D = (int)head_dim;
+  a.valid_len = valid_len == 0 ? (int)seq_len : (int)valid_len;
+  a.causal = causal ? 1 : 0;
+  a.scale = 1.0 / std::sqrt((double)head_dim);
+  if (dtype != AFA_F64) a.scale = (double)(float)a.scale;
+  a.omega = sink_omega;
+  hipError_t e = afa::generic_bwd_launch(dtype, a, s);
+  if (owned) {
+    hipError_t e2 = hipFreeAsync(ws, s);
+    if (e == hipSuccess) e = e2;
+  }
+  return hip_status(e);
+}
+
+int asoftmax_fwd(int dtype, int64_t rows, int64_t cols, const void* x, void* y,
+                 double sink_omega, double eps, void* stream) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (!x || !y) return AFA_ERR_NULL;
+  if (rows <= 0 || cols <= 0) return AFA_ERR_SHAPE;
+  if (!finite_nonneg(sink_omega)) return AFA_ERR_SINK;
+  if (!(eps > 0.0 && eps < INFINITY)) return AFA_ERR_EPS;
+  return hip_status(afa::asoftmax_fwd_launch(dtype, rows, cols, x, y, sink_omega, eps, (hipStream_t)stream));
+}
+
+int asoftmax_bwd(int dtype, int64_t rows, int64_t cols, const void* x, const void* g, void* dx,
+                 double sink_omega, double eps, void* stream) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (!x || !g || !dx) return AFA_ERR_NULL;
+  if (rows <= 0 || cols <= 0) return AFA_ERR_SHAPE;
+  if (!finite_nonneg(sink_omega)) return AFA_ERR_SINK;
+  if (!(eps > 0.0 && eps < INFINITY)) return AFA_ERR_EPS;
+  return hip_status(afa::asoftmax_bwd_launch(dtype, rows, cols, x, g, dx, sink_omega, eps, (hipStream_t)stream));
+}
+
+int octic_fwd(int dtype, int64_t n, const void* x, void* y, void* stream) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (!x || !y) return AFA_ERR_NULL;
+  if (n < 0) return AFA_ERR_SHAPE;
+  if (n == 0) return AFA_OK;
+  return hip_status(afa::octic_fwd_launch(dtype, n, x, y, (hipStream_t)stream));
+}
+
+int octic_bwd(int dtype, int64_t n, const void* x, const void* g, void* dx, void* stream) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (!x || !g || !dx) return AFA_ERR_NULL;
+  if (n < 0) return AFA_ERR_SHAPE;
+  if (n == 0) return AFA_OK;
+  return hip_status(afa::octic_bwd_launch(dtype, n, x, g, dx, (hipStream_t)stream));
+}
+
+int ago_build_tables(int table_dtype, int64_t dim, int64_t max_seq_len, const void* freqs,
+                     double base, void* cos_out, void* sin_out, void* stream) {
+  if (table_dtype != AFA_F32 && table_dtype != AFA_F64) return AFA_ERR_DTYPE;
+  if (!cos_out || !sin_out) return AFA_ERR_NULL;
+  if (dim <= 0 || dim % 2 != 0 || max_seq_len <= 0 || max_seq_len > INT32_MAX) return AFA_ERR_SHAPE;
+  return hip_status(afa::ago_tables_launch(table_dtype, (int)(dim / 2), (int)max_seq_len,
+                                           freqs, base, cos_out, sin_out,
+                                           (hipStream_t)stream));
+}
+
+int ago_rotate(int dtype, int64_t outer, int64_t seq_len, int64_t inner, int64_t dim,
+               const void* x, void* y, int table_dtype, const void* rot_cos,
+               const void* rot_sin, int64_t rot_len, void* stream) {
+  if (!valid_dtype(dtype) || !valid_dtype(table_dtype)) return AFA_ERR_DTYPE;
+  if (!x || !y || !rot_cos || !rot_sin) return AFA_ERR_NULL;
+  if (outer <= 0 || seq_len <= 0 || inner <= 0 || dim <= 0) return AFA_ERR_SHAPE;
+  if (dim % 2 != 0 || rot_len < seq_len) return AFA_ERR_ROTARY;
+  return hip_status(afa::ago_rotate_launch(dtype, table_dtype, outer, seq_len, inner, (int)dim, x, y,
+                                           rot_cos, rot_sin, (hipStream_t)stream));
+}
+
+}  // extern "C"

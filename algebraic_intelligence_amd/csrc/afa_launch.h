@@ -1,0 +1,73 @@
+// Kernel argument blocks and launcher prototypes shared by the kernels and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace afa {
+
+// Fused MFMA forward (afa_fwd_mfma.hip).
+struct FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* denom;
+  const float* rc;
+  const float* rs;
+  int64_t q_b, q_h, q_l, k_b, k_h, k_l, v_b, v_h, v_l, o_b, o_h, o_l;
+  int B, H, L;
+  int valid_len;    // keys >= valid_len carry zero weight (valid_len <= L)
+  int causal;
+  int nqb;          // query blocks per (b, h)
+  float q_scale;    // power of two folded into q
+  float omega;      // sink_omega times the weight scale
+  float w_unscale;  // denominator output = w_unscale * (D' + omega)
+};
+
+// Generic forward / backward (afa_generic.hip).
+struct GenArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out_in;  // backward: forward output
+  const void* dtot;    // backward: forward denominator (accumulation type)
+  const void* g;       // backward: output cotangent
+  void* out;           // forward output / backward dq
+  void* dk;
+  void* dv;
+  void* denom;         // forward denominator output (accumulation type), nullable
+  void* e_ws;          // backward: E workspace (accumulation type, B*H*L)
+  const void* rc;
+  const void* rs;
+  int64_t q_b, q_h, q_l, k_b, k_h, k_l, v_b, v_h, v_l, o_b, o_h, o_l;
+  int B, H, L, D;
+  int valid_len;
+  int causal;
+  int exact_ref;
+  double scale;
+  double omega;
+};
+
+bool mfma_fwd_supported(int dtype, int head_dim);
+int mfma_fwd_queries_per_block(int head_dim);
+hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
+
+hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
+hipError_t generic_bwd_launch(int dtype, const GenArgs& a, hipStream_t st);
+
+hipError_t ago_tables_launch(int table_dtype, int pairs, int len, const void* freqs, double base,
+                             void* c_out, void* s_out, hipStream_t st);
+hipError_t ago_rotate_launch(int dtype, int table_dtype, int64_t outer, int64_t seq, int64_t inner,
+                             int dim, const void* x, void* y, const void* rc, const void* rs,
+                             hipStream_t st);
+
+hipError_t asoftmax_fwd_launch(int dtype, int64_t rows, int64_t n, const void* x, void* y,
+                               double sink, double eps, hipStream_t st);
+hipError_t asoftmax_bwd_launch(int dtype, int64_t rows, int64_t n, const void* x, const void* g,
+                               void* dx, double sink, double eps, hipStream_t st);
+hipError_t octic_fwd_launch(int dtype, int64_t n, const void* x, void* y, hipStream_t st);
+hipError_t octic_bwd_launch(int dtype, int64_t n, const void* x, const void* g, void* dx,
+                            hipStream_t st);
+
+}  // namespace afa

@@ -1,0 +1,154 @@
+"""AFA forward benchmark on one MI355X (BASELINE.json metric, configuration C3).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (C3): B=8, H=12, L=4096, D=64, bf16, causal, q/k Cayley-rotated in-kernel with
+Cayley parameters t_i = 10000^(-2i/D); q, k, v ~ N(0, 1) synthetic, resident in HBM.
+A step is one fused forward launch (afa_fwd through the C ABI) over the whole batch.
+
+Printed: one JSON line with the whole-job throughput (TFLOP/s, FLOPs = 4 B H D L(L+1)/2),
+the roofline of the kernel (HIP-event average launch time on the launch stream against the
+2516.6 TFLOP/s bf16 dense MFMA peak) and the CPU baseline: the C restatement of the reference
+algorithm (oracle/afa_contract.c, OpenMP) timed on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "afa_fwd_c3_bf16_traffic.json")
+METRIC = "AFA fwd TFLOP/s + % bf16 MFMA peak at L=4096 D=64 (1 GPU); x vs host CPU ref"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    return ap.parse_args()
+
+
+def cpu_baseline(q, k, v, rot, seconds):
+    """Time the C contract restatement on whole (b, h) heads of the same inputs until the
+    budget is spent (at least one head); report TFLOP/s over the heads done."""
+    import numpy as np
+
+    from oracle import contract as C
+    from tests.helpers import to_bits
+
+    B, H, L, D = q.shape
+    cores = len(os.sched_getaffinity(0))
+    rc = rot.c.detach().cpu().numpy().astype(np.float32)
+    rs = rot.s.detach().cpu().numpy().astype(np.float32)
+    qb, kb, vb = (to_bits(t) for t in (q, k, v))
+    heads, elapsed = 0, 0.0
+    per_head_flops = 4 * D * L * (L + 1) // 2
+    while heads < B * H and (heads == 0 or elapsed < seconds):
+        b, h = divmod(heads, H)
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        t0 = time.perf_counter()
+        C.afa_fwd(qb[sl], kb[sl], vb[sl], C.DT_BF16, 0.5, True, None, (rc, rs), block_q=128, block_k=128,
+                  nthreads=cores)
+        elapsed += time.perf_counter() - t0
+        heads += 1
+    return {
+        "value": round(per_head_flops * heads / elapsed / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{heads} of {B * H} (b,h) heads of C3 (L={L}, D={D}, bf16, causal, AGO), "
+                  f"{elapsed:.1f} s, C restatement oracle/afa_contract.c with OpenMP",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: the AFA path's multi-GPU sharding "
+                                   "is a design note (DESIGN.md), so --gpus must be 1"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import algebraic_intelligence_amd as A
+    from algebraic_intelligence_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, H, L, D = 8, 12, 4096, 64
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn((B, H, L, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+               for _ in range(3))
+    freqs = 10000.0 ** (-2.0 * np.arange(D // 2) / D)
+    rot = A.build_cayley_rotary_matrix(D, L, freqs=freqs, device=dev)
+    rc, rs = rot.c.contiguous(), rot.s.contiguous()
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream(dev)
+    lib = _lib.lib()
+
+    def step():
+        r = lib.afa_fwd(_lib.AFA_BF16, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), None,
+                        out.data_ptr(), None, rc.data_ptr(), rs.data_ptr(), L, 0.5, 1, 0, 0,
+                        stream.cuda_stream)
+        if r != 0:
+            _lib.check(r, "afa_fwd")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(end)
+    ms = ms_total / args.steps
+    flops = A.afa_flops(B, H, L, D, causal=True)
+    tflops = flops / (ms * 1e-3) / 1e12
+    if not torch.isfinite(out.float()).all():
+        raise RuntimeError("non-finite output")
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: q,k,v ~ N(0,1) bf16, resident in HBM",
+        "config": {"workload": "C3: AFA forward, causal, Cayley rotary fused in-kernel", "batch": B,
+                   "heads": H, "seq_len": L, "head_dim": D, "sink_omega": 0.5,
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(q, k, v, rot, args.cpu_seconds)
+        line["cpu_baseline"]["gpu_speedup"] = round(tflops / line["cpu_baseline"]["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+/*
+ * afa.h — C ABI of the MI355X (gfx950) Algebraic FlashAttention library (libafa_hip.so).
+ *
+ * Every entry point takes plain device pointers, sizes and an optional hipStream_t
+ * (passed as void*; NULL = the default stream).  The caller owns every buffer; calls are
+ * stream-ordered, stateless and re-entrant.  They return 0 (AFA_OK) or an afa_status code;
+ * afa_status_string() gives the message.
+ *
+ * Layout: q, k, v, out are (batch, heads, seq_len, head_dim) with head_dim contiguous.
+ * `strides` (nullable) holds 12 element strides {q_b, q_h, q_l, k_b, k_h, k_l, v_b, v_h,
+ * v_l, o_b, o_h, o_l}; NULL means contiguous.  The denominator output is contiguous
+ * (batch, heads, seq_len) fp32 (fp64 for AFA_F64 inputs).
+ *
+ * Citations are into tasmaikeni13/algebraic-intelligence.
+ */
+#ifndef ALGEBRAIC_INTELLIGENCE_AMD_AFA_H
+#define ALGEBRAIC_INTELLIGENCE_AMD_AFA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types; AFA_F64 accumulates in fp64 like the reference (pallas_afa.py:208). */
+enum afa_dtype { AFA_F32 = 0, AFA_BF16 = 1, AFA_F16 = 2, AFA_F64 = 3 };
+
+enum afa_status {
+  AFA_OK = 0,
+  AFA_ERR_NULL = 1,          /* a required pointer is NULL */
+  AFA_ERR_DTYPE = 2,         /* unsupported dtype */
+  AFA_ERR_SHAPE = 3,         /* non-positive or inconsistent sizes */
+  AFA_ERR_HEAD_DIM = 4,      /* head_dim > 128 and not a multiple of 128 (pallas_afa.py:179-180) */
+  AFA_ERR_SINK = 5,          /* sink_omega not finite or negative (pallas_afa.py:171-172) */
+  AFA_ERR_VALID_LEN = 6,     /* valid_len outside [1, seq_len] (pallas_afa.py:185-186) */
+  AFA_ERR_EPS = 7,           /* eps not finite or not positive (attention.py:62-63) */
+  AFA_ERR_ROTARY = 8,        /* rotary tables shorter than seq_len, or odd head_dim */
+  AFA_ERR_ALIGN = 9,         /* a stride or pointer breaks the required alignment */
+  AFA_ERR_WORKSPACE = 10,    /* workspace too small */
+  AFA_ERR_UNSUPPORTED = 11,  /* combination this build does not implement */
+  AFA_ERR_HIP = 100          /* a HIP runtime call failed; afa_last_hip_error() has the code */
+};
+
+/* Flags for afa_fwd / afa_bwd. */
+#define AFA_FLAG_EXACT_TAIL 0x1u   /* always use the cancellation-safe two-branch rho for s < 0 */
+#define AFA_FLAG_GENERIC 0x2u      /* route to the generic (non-MFMA) kernel */
+#define AFA_FLAG_EXACT_REF 0x4u    /* exact_afa_reference contract: q*scale rounded to the input
+                                      dtype before the dot, row sum of P cast to v.dtype, and
+                                      out = o * (1/(D+Omega)) (pallas_afa.py:283-297) */
+
+const char* afa_status_string(int status);
+int afa_last_hip_error(void);
+int afa_version(void);
+
+/*
+ * Fused AFA forward.  Replaces pallas_afa_forward (src/kernels/pallas_afa.py:154-264) and its
+ * tile kernel afa_kernel (:52-151); also serves tiled_afa_forward (:330-406), whose result is
+ * the same function of the inputs.  out = sum_j rho(s_ij)^8 v_j / (sum_j rho(s_ij)^8 + sink),
+ * s_ij = q_i.k_j / sqrt(head_dim); keys j > i are masked when causal != 0 and keys
+ * j >= valid_len when valid_len > 0.  denom (nullable) receives sum_j rho^8 + sink.
+ * rot_cos/rot_sin (nullable, both or neither): Cayley rotary tables (rot_len, head_dim/2),
+ * fp32 (fp64 for AFA_F64); q and k rows at position i are rotated by row i at tile load
+ * (fusing _rotate_tensor, src/attention.py:142-152, as called from src/model.py:262-264).
+ */
+int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+            const void* q, const void* k, const void* v, const int64_t* strides, void* out,
+            void* denom, const void* rot_cos, const void* rot_sin, int64_t rot_len,
+            double sink_omega, int causal, int64_t valid_len, unsigned flags, void* stream);
+
+/*
+ * Analytical AFA backward.  Replaces tiled_afa_backward (src/kernels/pallas_afa.py:409-522)
+ * as used by the pallas_afa custom VJP (:532-615).  Inputs: the forward's q, k, v, out and
+ * denom (= d_total, fp32; fp64 for AFA_F64) and the output cotangent g (same layout as q).
+ * Outputs dq, dk, dv (contiguous).  With rotary tables the forward rotated q and k, and the
+ * returned dq, dk are with respect to the unrotated inputs.  workspace: at least
+ * afa_bwd_workspace_size() bytes of device memory, or NULL to let the call allocate and free
+ * it on `stream`.
+ */
+size_t afa_bwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                              int64_t head_dim);
+int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+            const void* q, const void* k, const void* v, const void* out, const void* denom,
+            const void* g, void* dq, void* dk, void* dv, const void* rot_cos,
+            const void* rot_sin, int64_t rot_len, double sink_omega, int causal,
+            int64_t valid_len, unsigned flags, void* workspace, size_t workspace_bytes,
+            void* stream);
+
+/*
+ * A-Softmax over the last axis of a (rows, cols) contiguous array: AVN normalisation
+ * tau = rsqrt(mean(x^2) + eps), then rho(tau x)^8 / (sum + sink), in fp32 (fp64 for AFA_F64),
+ * output in the input dtype.  Replaces algebraic_softmax (src/attention.py:53-91, with AVN from
+ * src/primitives.py:56-65).  asoftmax_bwd is its cached VJP (src/attention.py:75-82 with
+ * src/primitives.py:73-79).
+ */
+int asoftmax_fwd(int dtype, int64_t rows, int64_t cols, const void* x, void* y,
+                 double sink_omega, double eps, void* stream);
+int asoftmax_bwd(int dtype, int64_t rows, int64_t cols, const void* x, const void* g, void* dx,
+                 double sink_omega, double eps, void* stream);
+
+/* Elementwise rho(x)^8 and its VJP 8 r rho^8 g.  Replaces octic_kernel / _vmu_octic_kernel
+ * (src/attention.py:18-50, src/kernels/pallas_afa.py:32-49). */
+int octic_fwd(int dtype, int64_t n, const void* x, void* y, void* stream);
+int octic_bwd(int dtype, int64_t n, const void* x, const void* g, void* dx, void* stream);
+
+/*
+ * Cayley rotary tables.  Replaces build_cayley_rotary_matrix (src/attention.py:155-204):
+ * c, s of shape (max_seq_len, dim/2) in table_dtype (AFA_F32 or AFA_F64, device memory).
+ * freqs (nullable, device memory, dim/2 entries of table_dtype) are the Cayley parameters w_k;
+ * NULL selects the default w_k = 1/(1 + alpha k)^2, alpha = (sqrt(base) - 1)/max(dim/2 - 1, 1).
+ */
+int ago_build_tables(int table_dtype, int64_t dim, int64_t max_seq_len, const void* freqs,
+                     double base, void* cos_out, void* sin_out, void* stream);
+
+/*
+ * Pairwise Cayley rotation of x viewed as (outer, seq_len, inner, dim), contiguous, by the
+ * table row of each sequence position.  The tables (rot_len >= seq_len rows, dim/2 columns,
+ * table_dtype AFA_F32/AFA_BF16/AFA_F16/AFA_F64) are cast to the x dtype first, as
+ * _rotate_tensor does (src/attention.py:142-152); apply_ago_rotations (:207-240) calls this for
+ * q and k.  y may alias x.
+ */
+int ago_rotate(int dtype, int64_t outer, int64_t seq_len, int64_t inner, int64_t dim,
+               const void* x, void* y, int table_dtype, const void* rot_cos,
+               const void* rot_sin, int64_t rot_len, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ALGEBRAIC_INTELLIGENCE_AMD_AFA_H */

@@ -1,0 +1,208 @@
+"""GPU parity of the fused AFA forward against the oracles (float64 numpy and the C contract).
+
+Configurations follow BASELINE.json (C1..C5); tolerances are the north-star ones (fp32 1e-5,
+bf16 2e-2 normwise against float64 on identical inputs) plus tighter bounds against the C
+restatement of the kernel's dtype contract.  Every call goes through the C ABI (afa_fwd).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import afa_oracle as O
+from tests.helpers import make_qkv, normwise, oracle_contract, to_f64
+
+pytestmark = pytest.mark.gpu
+
+import algebraic_intelligence_amd as A  # noqa: E402
+from algebraic_intelligence_amd import _lib  # noqa: E402
+
+
+def _fwd(q, k, v, sink=0.5, causal=False, valid=None, rotary=None, flags=0):
+    """Direct afa_fwd call returning (out, denominator)."""
+    return A.afa._launch_fwd(q, k, v, sink, causal, valid, rotary, flags, True)
+
+
+def _c3_freqs(D):
+    """Config-3 Cayley parameters t_i = 10000^(-2i/D), computed in fp64 on the host."""
+    return 10000.0 ** (-2.0 * np.arange(D // 2) / D)
+
+
+# ----------------------------------------------------------------------------------- fp32 / fp64
+def test_c1_fp32_noncausal_vs_fp64():
+    q, k, v = make_qkv((1, 4, 256, 64), torch.float32, seed=0)
+    out, den = _fwd(q, k, v)
+    ref, dref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, False, return_denominator=True)
+    err = normwise(to_f64(out), ref)
+    print("C1 fp32 err", err)
+    assert err <= 1e-5
+    assert normwise(to_f64(den), dref) <= 1e-5
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp64_vs_oracle(causal):
+    q, k, v = make_qkv((1, 2, 256, 64), torch.float64, seed=102)
+    out, den = _fwd(q, k, v, causal=causal)
+    ref, dref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, causal, return_denominator=True)
+    assert out.dtype == torch.float64 and den.dtype == torch.float64
+    assert normwise(to_f64(out), ref) <= 1e-12
+    assert normwise(to_f64(den), dref) <= 1e-12
+
+
+# ----------------------------------------------------------------------------------- bf16 MFMA
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_small_vs_contract_and_fp64(causal):
+    q, k, v = make_qkv((1, 4, 256, 64), torch.bfloat16, seed=1)
+    out, den = _fwd(q, k, v, causal=causal)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal)
+    ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, causal)
+    e_c, e_r = normwise(to_f64(out), c_out), normwise(to_f64(out), ref)
+    print(f"bf16 small causal={causal}: vs contract {e_c:.3e} vs fp64 {e_r:.3e}")
+    assert e_c <= 4e-3
+    assert e_r <= 2e-2
+    assert normwise(to_f64(den), c_den) <= 1e-5
+
+
+def test_c2_bf16_causal():
+    """C2: B=4 H=8 L=2048 D=64 bf16 causal, q,k,v ~ N(0,1)/sqrt(D)."""
+    q, k, v = make_qkv((4, 8, 2048, 64), torch.bfloat16, seed=2, scale=1 / 8)
+    out, den = _fwd(q, k, v, causal=True)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, True)
+    e_c = normwise(to_f64(out), c_out)
+    ref = O.afa_forward(to_f64(q[:1, :2]), to_f64(k[:1, :2]), to_f64(v[:1, :2]), 0.5, True)
+    e_r = normwise(to_f64(out[:1, :2]), ref)
+    print(f"C2: vs contract {e_c:.3e}, vs fp64 (2 heads) {e_r:.3e}")
+    assert e_c <= 4e-3 and e_r <= 2e-2
+    assert normwise(to_f64(den), c_den) <= 1e-5
+
+
+def test_c2_outlier_keys():
+    """C2 outlier variant: a seeded 1% of k rows per (b, h) multiplied by 20 (in fp32, rounded once)."""
+    B, H, L, D = 4, 8, 2048, 64
+    rng = np.random.default_rng(22)
+    q, k, v = (rng.standard_normal((B, H, L, D)) / 8 for _ in range(3))
+    k = k.astype(np.float32)
+    for b in range(B):
+        for h in range(H):
+            rows = rng.choice(L, size=L // 100, replace=False)
+            k[b, h, rows] *= np.float32(20.0)
+    q, k, v = (torch.from_numpy(np.asarray(x)).to(torch.bfloat16).cuda() for x in (q, k, v))
+    out, den = _fwd(q, k, v, causal=True)
+    c_out, _ = oracle_contract(q, k, v, 0.5, True)
+    ref = O.afa_forward(to_f64(q[:1, :2]), to_f64(k[:1, :2]), to_f64(v[:1, :2]), 0.5, True)
+    e_c, e_r = normwise(to_f64(out), c_out), normwise(to_f64(out[:1, :2]), ref)
+    print(f"C2 outlier: vs contract {e_c:.3e}, vs fp64 {e_r:.3e}")
+    assert np.isfinite(to_f64(out)).all()
+    assert e_c <= 4e-3 and e_r <= 2e-2
+
+
+def test_c3_fused_ago_full_size():
+    """C3 (north star): B=8 H=12 L=4096 D=64 bf16 causal, AGO with t_i = 10000^(-2i/D) fused."""
+    B, H, L, D = 8, 12, 4096, 64
+    q, k, v = make_qkv((B, H, L, D), torch.bfloat16, seed=3)
+    rot = A.build_cayley_rotary_matrix(D, L, freqs=_c3_freqs(D))
+    out, den = _fwd(q, k, v, causal=True, rotary=rot)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, True, rotary=rot)
+    e_c = normwise(to_f64(out), c_out)
+    # fp64 end-to-end on two heads: fp64 tables, fp64 rotation of the same bf16 inputs
+    ct, st = O.cayley_tables(D, L, freqs=_c3_freqs(D))
+    ref = O.afa_forward(to_f64(q[:1, :2]), to_f64(k[:1, :2]), to_f64(v[:1, :2]), 0.5, True, rotary=(ct, st))
+    e_r = normwise(to_f64(out[:1, :2]), ref)
+    print(f"C3: vs contract {e_c:.3e}, vs fp64 (2 heads) {e_r:.3e}")
+    assert e_c <= 4e-3 and e_r <= 2e-2
+    assert normwise(to_f64(den), c_den) <= 1e-4
+
+
+# ----------------------------------------------------------------------------------- invariants
+def test_causal_prefix_invariance_is_bitwise():
+    """Perturbing keys/values at positions >= 150 leaves outputs < 150 bit-identical
+    (tests/test_pallas_afa.py:151-158)."""
+    for dt in (torch.float32, torch.bfloat16):
+        q, k, v = make_qkv((1, 1, 256, 64), dt, seed=104)
+        y = A.pallas_afa_forward(q, k, v, causal=True)
+        k2, v2 = k.clone(), v.clone()
+        k2[:, :, 150:] += 10.0
+        v2[:, :, 150:] += 10.0
+        y2 = A.pallas_afa_forward(q, k2, v2, causal=True)
+        assert torch.equal(y[:, :, :150], y2[:, :, :150])
+
+
+def test_block_arguments_do_not_change_results():
+    q, k, v = make_qkv((1, 2, 256, 64), torch.bfloat16, seed=106)
+    y128 = A.tiled_afa_forward(q, k, v, block_q=128, block_k=128)
+    y64 = A.tiled_afa_forward(q, k, v, block_q=64, block_k=64)
+    y32 = A.pallas_afa_forward(q, k, v, block_q=32, block_k=64)
+    assert torch.equal(y128, y64) and torch.equal(y128, y32)
+
+
+@pytest.mark.parametrize("L,bq,bk", [(180, 128, 128), (190, 64, 128)])
+def test_arbitrary_length_front_door(L, bq, bk):
+    """algebraic_flash_attention on lengths that are not tile multiples
+    (tests/test_pallas_afa.py:173-198)."""
+    for dt, tol in ((torch.float32, 1e-5), (torch.bfloat16, 2e-2)):
+        q, k, v = make_qkv((1, 2, L, 64), dt, seed=105)
+        y = A.algebraic_flash_attention(q, k, v, block_q=bq, block_k=bk)
+        ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, False)
+        assert y.shape == q.shape
+        assert normwise(to_f64(y), ref) <= tol
+
+
+def test_valid_seq_len_masks_keys():
+    q, k, v = make_qkv((2, 2, 256, 64), torch.bfloat16, seed=7)
+    for causal in (False, True):
+        y = A.pallas_afa_forward(q, k, v, causal=causal, valid_seq_len=200)
+        c_out, _ = oracle_contract(q, k, v, 0.5, causal, valid_len=200)
+        ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, causal, valid_len=200)
+        assert normwise(to_f64(y), c_out) <= 4e-3
+        assert normwise(to_f64(y), ref) <= 2e-2
+
+
+def test_strided_model_layout_matches_contiguous():
+    """q, k, v as (B, T, H, D).transpose(1, 2) views (the model's layout, src/model.py:257-260)."""
+    B, T, H, D = 2, 512, 4, 64
+    rng = np.random.default_rng(9)
+    base = [torch.from_numpy(rng.standard_normal((B, T, H, D))).to(torch.bfloat16).cuda() for _ in range(3)]
+    views = [x.transpose(1, 2) for x in base]
+    y_view = A.pallas_afa_forward(*views, causal=True)
+    y_cont = A.pallas_afa_forward(*[x.contiguous() for x in views], causal=True)
+    assert torch.equal(y_view, y_cont)
+
+
+def test_mfma_matches_generic_kernel():
+    """The MFMA kernel and the generic kernel are independent implementations of one contract."""
+    q, k, v = make_qkv((2, 3, 512, 64), torch.bfloat16, seed=11)
+    for causal in (False, True):
+        a, da = _fwd(q, k, v, causal=causal)
+        b, db = _fwd(q, k, v, causal=causal, flags=_lib.FLAG_GENERIC)
+        assert normwise(to_f64(a), to_f64(b)) <= 4e-3
+        assert normwise(to_f64(da), to_f64(db)) <= 1e-5
+
+
+def test_exact_tail_flag_agrees():
+    q, k, v = make_qkv((1, 4, 512, 64), torch.bfloat16, seed=12)
+    a, _ = _fwd(q, k, v, causal=True)
+    b, _ = _fwd(q, k, v, causal=True, flags=_lib.FLAG_EXACT_TAIL)
+    ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, True)
+    assert normwise(to_f64(a), ref) <= 2e-2 and normwise(to_f64(b), ref) <= 2e-2
+    assert normwise(to_f64(a), to_f64(b)) <= 4e-3
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_head_dim_128(dt):
+    """C5-shaped forward (D=128) at reduced size.  fp16 inputs are scaled so that rho^8 stays
+    below the fp16 overflow threshold when P is cast to v.dtype (the reference casts the same way)."""
+    q, k, v = make_qkv((1, 4, 512, 128), dt, seed=13, scale=1.0 if dt == torch.bfloat16 else 0.3)
+    out, den = _fwd(q, k, v, causal=True)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, True)
+    ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, True)
+    print(f"D=128 {dt}: vs contract {normwise(to_f64(out), c_out):.3e} vs fp64 {normwise(to_f64(out), ref):.3e}")
+    assert normwise(to_f64(out), c_out) <= 4e-3
+    assert normwise(to_f64(out), ref) <= 2e-2
+    assert normwise(to_f64(den), c_den) <= 1e-5
+
+
+@pytest.mark.parametrize("D", [8, 16, 32, 48, 96, 256])
+def test_generic_head_dims(D):
+    q, k, v = make_qkv((1, 2, 96, D), torch.float32, seed=14)
+    y = A.pallas_afa_forward(q, k, v, causal=True, block_q=32, block_k=32)
+    ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, True)
+    assert normwise(to_f64(y), ref) <= 1e-5
