@@ -47,7 +47,9 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) - 1), 8)
     with cf.ThreadPoolExecutor(jobs) as ex:
         list(ex.map(lambda so: _compile(so[0], so[1], verbose), zip(srcs, objs)))
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB + ".tmp"]
+    # --no-undefined: a kernel whose host stub was not emitted must fail here, not at load time
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", *objs,
+           "-o", LIB + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

@@ -124,6 +124,10 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     a.q_scale = 1.0f;
     a.w_unscale = 1.0f;
     const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, vlen);
+    if (head_dim == 64 && !(flags & AFA_FLAG_SIMPLE_SCHEDULE)) {
+      a.nqb = (int)((seq_len + 255) / 256);
+      return hip_status(afa::d64_fwd_launch(dtype, a, exact, s));
+    }
     return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
   }
   if (head_dim > 256) return AFA_ERR_UNSUPPORTED;

@@ -1,0 +1,396 @@
+// Software-pipelined fused AFA forward for head_dim 64 (bf16 / fp16 operands, fp32 accumulate).
+//
+// Same contract as afa_fwd_mfma.hip (src/kernels/pallas_afa.py:52-151); this kernel is shaped
+// for the VALU-bound regime of head_dim 64, where each score costs ~7 VALU slots (rho^8 chain,
+// row sum, bf16 pack) against 256 MFMA FLOPs:
+//
+//   * a wave owns 64 queries = two 32-query blocks; its key axis is cut into 32-key sub-tiles,
+//     and a "unit" is (sub-tile n, query block qb), u = 2n + qb;
+//   * unit u evaluates rho^8 of S(u) on the VALU while the MFMA pipe runs S(u+1) = K Q^T and
+//     O += V^T P(u-1); sched_group_barrier interleaves the 8 MFMAs with the ~150 VALU ops;
+//   * K tiles (Cayley-rotated on their way in) are row-major with 16 B row padding; V tiles are
+//     row-major with their two 64 B halves XOR-swizzled by (row >> 1) & 1 and are read with
+//     ds_read_tr16_b64, which returns 4 consecutive keys of one feature column per lane: two
+//     such reads form the PV MFMA's A operand in the key order of the S^T accumulator;
+//   * LDS holds 3 tiles of 64 keys: tile t+2 is stored at the end of tile t's iteration, into the
+//     buffer tile t-1 used, and a single barrier per tile orders reads and stores;
+//   * masks (causal diagonal, valid_len) are applied only on units that cross them.
+#include <type_traits>
+
+#include "afa_common.h"
+#include "afa_launch.h"
+
+namespace afa {
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+template <int DT>
+__device__ __forceinline__ f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (DT == AFA_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4_t rot4(u32x4_t w, f32x4_t c, f32x4_t s, float scale) {
+#pragma clang fp contract(off)
+  u32x4_t r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float x0 = Elem<DT>::lo(w[p]);
+    const float x1 = Elem<DT>::hi(w[p]);
+    const float y0 = c[p] * x0 - s[p] * x1;
+    const float y1 = s[p] * x0 + c[p] * x1;
+    r[p] = Elem<DT>::pack(y0 * scale, y1 * scale);
+  }
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4_t scl4(u32x4_t w, float scale) {
+  u32x4_t r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r[p] = Elem<DT>::pack(Elem<DT>::lo(w[p]) * scale, Elem<DT>::hi(w[p]) * scale);
+  return r;
+}
+
+// Pairwise tree sum of 16 values (shorter dependency chain than a running sum).
+__device__ __forceinline__ float tree16(const float (&p)[16]) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = p[2 * i] + p[2 * i + 1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = a[2 * i] + a[2 * i + 1];
+  a[0] = a[0] + a[1];
+  a[2] = a[2] + a[3];
+  return a[0] + a[2];
+}
+
+}  // namespace
+
+template <int DT, bool EXACT, bool ROT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void afa_fwd_d64_kernel(const FwdArgs a) {
+  constexpr int D = 64;
+  constexpr int KT = 64;        // keys per LDS tile
+  constexpr int NB = 3;         // LDS tile buffers
+  constexpr int KSTR = D + 8;   // K row stride (elements)
+  __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * KSTR];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * D];
+  // staging area of the next K tile: raw rows and their Cayley table rows, filled by direct
+  // global -> LDS loads; slot c (16 B) belongs to thread chunk c
+  __shared__ __attribute__((aligned(16))) unsigned short lds_kraw[KT * D];
+  __shared__ __attribute__((aligned(16))) float lds_c[ROT ? KT * D / 2 : 4];
+  __shared__ __attribute__((aligned(16))) float lds_s[ROT ? KT * D / 2 : 4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  const int l16 = lane & 15;
+  const int m16 = (lane >> 4) & 1;
+
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = item / a.nqb;
+  const int qblk = a.causal ? (a.nqb - 1 - item % a.nqb) : (item % a.nqb);
+  const int b = bh / a.H;
+  const int h = bh % a.H;
+  const int L = a.L;
+  const int vlen = a.valid_len;
+
+  const int q0_wg = qblk * 256;
+  const int q0_w = q0_wg + wave * 64;
+  const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 256)) : vlen;
+  const int kend_w = a.causal ? min(vlen, q0_w + 64) : vlen;
+  const int ntiles = (kend_wg + KT - 1) / KT;
+  const int nsub = q0_w < L ? (kend_w + 31) / 32 : 0;  // 32-key sub-tiles of this wave
+  const int U = 2 * nsub;                                // units of this wave
+
+  const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
+  const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
+  const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
+
+  // ---- Q fragments: query q0_w + qb*32 + l32, features kc*16 + 8g .. +7 (scaled, rotated)
+  u32x4_t qf[2][4];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qi = q0_w + qb * 32 + l32;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const int d0 = kc * 16 + 8 * g;
+      u32x4_t w = {0u, 0u, 0u, 0u};
+      if (qi < L) {
+        w = *(const u32x4_t*)(qp + (int64_t)qi * a.q_l + d0);
+        if constexpr (ROT) {
+          const f32x4_t c = *(const f32x4_t*)(a.rc + (int64_t)qi * (D / 2) + d0 / 2);
+          const f32x4_t s = *(const f32x4_t*)(a.rs + (int64_t)qi * (D / 2) + d0 / 2);
+          w = rot4<DT>(w, c, s, a.q_scale);
+        } else {
+          w = scl4<DT>(w, a.q_scale);
+        }
+      }
+      qf[qb][kc] = w;
+    }
+  }
+
+  // ---- tile staging, all by direct global -> LDS loads (no staging registers).  Thread chunk
+  // c = tid + 256 i covers key row c >> 3, 16-byte column c & 7, and a wave's loads fill one
+  // contiguous 1 KB stripe (lane slot = chunk).  V lands in its swizzled position: slot
+  // (row, physical chunk pc) receives logical chunk pc ^ (((row >> 1) & 1) << 2).  K lands raw;
+  // each thread rotates its own chunks into the K tile after its loads complete (finish_k).
+  // Rows past L read row L-1: those keys are masked, the data only has to be finite.
+  auto issue_tile = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 3, c8 = c & 7;
+      const int key = min(t * KT + row, L - 1);
+      const int stripe = (256 * i + wave * 64);  // first chunk of this wave's stripe
+      const int lc = c8 ^ (((row >> 1) & 1) << 2);
+      // (the builtin takes untyped pointers; typed ones make the host pass drop the kernel stub)
+      __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lc * 8),
+                                       (void*)&lds_v[t % NB][stripe * 8], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + c8 * 8),
+                                       (void*)&lds_kraw[stripe * 8], 16, 0, 0);
+      if constexpr (ROT) {
+        __builtin_amdgcn_global_load_lds((const void*)(a.rc + (int64_t)key * (D / 2) + c8 * 4),
+                                         (void*)&lds_c[stripe * 4], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(a.rs + (int64_t)key * (D / 2) + c8 * 4),
+                                         (void*)&lds_s[stripe * 4], 16, 0, 0);
+      }
+    }
+  };
+  auto finish_k = [&](int t) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's direct loads have landed
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 3, c8 = c & 7;
+      u32x4_t kw = *(const u32x4_t*)&lds_kraw[c * 8];
+      if constexpr (ROT) {
+        const f32x4_t cc = *(const f32x4_t*)&lds_c[c * 4];
+        const f32x4_t ss = *(const f32x4_t*)&lds_s[c * 4];
+        kw = rot4<DT>(kw, cc, ss, 1.0f);
+      }
+      *(u32x4_t*)&lds_k[t % NB][row * KSTR + c8 * 8] = kw;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // staging reads done before the next direct loads
+  };
+
+  // ---- per-unit fragment readers
+  // K fragment (A operand of S^T = K Q^T) of sub-tile n: key (n&1)*32 + l32 of its tile.
+  auto read_kf = [&](int n, u32x4_t (&kf)[4]) {
+    const unsigned short* base = &lds_k[(n >> 1) % NB][((n & 1) * 32 + l32) * KSTR + 8 * g];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) kf[kc] = *(const u32x4_t*)(base + kc * 16);
+  };
+  // V^T fragments (A operand of O^T = V^T P^T) of sub-tile n: feature db*32 + l32, keys in the
+  // S^T accumulator order: half kk, elements e -> key kk*16 + (e>>2)*8 + 4g + (e&3).
+  auto read_vf = [&](int n, u32x4_t (&vf)[2][2]) {
+    const unsigned short* tile = lds_v[(n >> 1) % NB];
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        u32x4_t f;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int row = (n & 1) * 32 + kk * 16 + hh * 8 + 4 * g + (l16 >> 2);
+          const int blk = db ^ ((row >> 1) & 1);
+          const unsigned short* p = tile + row * D + blk * 32 + m16 * 16 + 4 * (l16 & 3);
+          const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+          const u32x2_t w = __builtin_bit_cast(u32x2_t, v);
+          f[2 * hh] = w[0];
+          f[2 * hh + 1] = w[1];
+        }
+        vf[db][kk] = f;
+      }
+    }
+  };
+
+  f32x16_t o[2][2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[db][qb][e] = 0.f;
+  float rowsum[2] = {0.f, 0.f};
+
+  // pipeline state
+  f32x16_t s_cur;       // S^T of the current unit (turned into P by it)
+  u32x4_t p_prev[2];    // packed P of the previous unit (kk halves)
+  u32x4_t kf[4];        // K fragments of the sub-tile of the next unit
+  u32x4_t vf[2][2];     // V^T fragments of the sub-tile of the previous unit
+
+  // ---- prologue: tiles 0 and 1 into LDS
+  if (ntiles > 0) {
+    issue_tile(0);
+    finish_k(0);
+  }
+  if (ntiles > 1) {
+    issue_tile(1);
+    finish_k(1);
+  }
+  __syncthreads();
+
+  auto rho16 = [&](float (&p)[16]) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = EXACT ? rho8_exact(s_cur[r]) : rho8_fast(s_cur[r]);
+  };
+  auto mask16 = [&](float (&p)[16], int u) {
+    const int key0 = (u >> 1) * 32;
+    const int qlo = q0_w + (u & 1) * 32;
+    if ((a.causal && key0 + 31 > qlo) || key0 + 31 >= vlen) {
+      const int qi = qlo + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = key0 + (r >> 2) * 8 + 4 * g + (r & 3);
+        const bool keep = (j < vlen) && (!a.causal || j <= qi);
+        p[r] = keep ? p[r] : 0.f;
+      }
+    }
+  };
+  auto finish_p = [&](float (&p)[16], int qb) {
+    rowsum[qb] += tree16(p);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p_prev[kk][e] = Elem<DT>::pack(p[kk * 8 + 2 * e], p[kk * 8 + 2 * e + 1]);
+  };
+
+  // ---- unit 0 (prologue): S(0), P(0), S(1); fragments K(1), V(0)
+  if (U > 0) {
+    read_kf(0, kf);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s_cur[e] = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) s_cur = mma<DT>(kf[kc], qf[0][kc], s_cur);
+    f32x16_t s_nxt;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s_nxt[e] = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) s_nxt = mma<DT>(kf[kc], qf[1][kc], s_nxt);
+    float p[16];
+    rho16(p);
+    mask16(p, 0);
+    finish_p(p, 0);
+    s_cur = s_nxt;
+    read_kf(1, kf);
+    read_vf(0, vf);
+  }
+
+  // Unit u = 2n + QB (QB compile-time): P(u) from s_cur; S(u+1) and PV(u-1) on the MFMA pipe,
+  // interleaved with the rho^8 VALU; even units then read the fragments of sub-tiles n+1 (K)
+  // and n (V).  The last two units of a wave take the guarded tail path.
+  auto unit = [&](int u, auto qb_tag) {
+    constexpr int QB = decltype(qb_tag)::value;
+    constexpr int NQ = QB ^ 1;   // query block of unit u+1
+    constexpr int PQ = QB ^ 1;   // query block of unit u-1
+    if (u > U) return;
+    const int n = u >> 1;
+    if (u + 1 < U) {
+      f32x16_t s_nxt;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s_nxt[e] = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) s_nxt = mma<DT>(kf[kc], qf[NQ][kc], s_nxt);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) o[db][PQ] = mma<DT>(vf[db][kk], p_prev[kk], o[db][PQ]);
+      float p[16];
+      rho16(p);
+      if constexpr (QB == 0) {
+        read_kf(n + 1, kf);
+        read_vf(n, vf);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);    // VALU lead-in
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // ~10 VALU
+      }
+      if constexpr (QB == 0) __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // fragment reads
+      mask16(p, u);
+      finish_p(p, QB);
+      s_cur = s_nxt;
+    } else {
+      // tail: PV(u-1) always (u >= 1), P(u) when u < U
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) o[db][PQ] = mma<DT>(vf[db][kk], p_prev[kk], o[db][PQ]);
+      if (u < U) {
+        float p[16];
+        rho16(p);
+        mask16(p, u);
+        finish_p(p, QB);
+        if constexpr (QB == 0) read_vf(n, vf);
+      }
+    }
+  };
+
+  // Tile t+2 goes into the buffer of tile t-1, whose last reads happened before the previous
+  // barrier; it is complete and visible after this iteration's barrier, one iteration before
+  // its first read.  Iteration t runs units 4t+1 .. 4t+4 (reading tiles t and t+1).
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 2 < ntiles) issue_tile(t + 2);
+    for (int hh = 0; hh < 2; ++hh) {
+      unit(4 * t + 2 * hh + 1, std::integral_constant<int, 1>{});
+      unit(4 * t + 2 * hh + 2, std::integral_constant<int, 0>{});
+    }
+    if (t + 2 < ntiles) finish_k(t + 2);
+    __syncthreads();
+  }
+
+  // ---- epilogue
+  unsigned short* op = (unsigned short*)a.out + b * a.o_b + h * a.o_h;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float tot = rowsum[qb] + __shfl_xor(rowsum[qb], 32) + a.omega;
+    const int qi = q0_w + qb * 32 + l32;
+    if (qi < L) {
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int d0 = db * 32 + r4 * 8 + 4 * g;
+          u32x2_t w;
+          w[0] = Elem<DT>::pack(o[db][qb][r4 * 4 + 0] / tot, o[db][qb][r4 * 4 + 1] / tot);
+          w[1] = Elem<DT>::pack(o[db][qb][r4 * 4 + 2] / tot, o[db][qb][r4 * 4 + 3] / tot);
+          *(u32x2_t*)(op + (int64_t)qi * a.o_l + d0) = w;
+        }
+      }
+      if (a.denom != nullptr && g == 0) a.denom[(int64_t)bh * L + qi] = tot * a.w_unscale;
+    }
+  }
+}
+
+template <int DT, bool EXACT, bool ROT>
+static hipError_t launch_d64(const FwdArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((afa_fwd_d64_kernel<DT, EXACT, ROT>), dim3(a.B * a.H * a.nqb), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream) {
+  a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
+  a.w_unscale = 1.0f;
+  const bool rot = a.rc != nullptr;
+  if (dtype == AFA_BF16) {
+    if (exact) return rot ? launch_d64<AFA_BF16, true, true>(a, stream) : launch_d64<AFA_BF16, true, false>(a, stream);
+    return rot ? launch_d64<AFA_BF16, false, true>(a, stream) : launch_d64<AFA_BF16, false, false>(a, stream);
+  }
+  if (exact) return rot ? launch_d64<AFA_F16, true, true>(a, stream) : launch_d64<AFA_F16, true, false>(a, stream);
+  return rot ? launch_d64<AFA_F16, false, true>(a, stream) : launch_d64<AFA_F16, false, false>(a, stream);
+}
+
+}  // namespace afa

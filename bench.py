@@ -34,7 +34,21 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run a plain device copy of MIB MiB --steps times "
+                         "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def copy_calibration(mib, steps):
+    import torch
+
+    src = torch.ones(mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "steps": steps}), flush=True)
 
 
 def cpu_baseline(q, k, v, rot, seconds):
@@ -76,6 +90,10 @@ def main():
         print(json.dumps({"error": "this build measures one GPU: the AFA path's multi-GPU sharding "
                                    "is a design note (DESIGN.md), so --gpus must be 1"}))
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, args.steps)
+        return
 
     import numpy as np
     import torch

@@ -206,3 +206,30 @@ def test_generic_head_dims(D):
     y = A.pallas_afa_forward(q, k, v, causal=True, block_q=32, block_k=32)
     ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, True)
     assert normwise(to_f64(y), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("shape,causal,valid", [
+    ((1, 1, 1, 64), True, None), ((1, 1, 32, 64), False, None), ((2, 3, 96, 64), True, None),
+    ((1, 2, 300, 64), True, None), ((1, 2, 300, 64), False, 257), ((3, 5, 513, 64), True, 400),
+    ((1, 1, 1024, 64), False, None), ((2, 4, 1000, 64), True, None),
+])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_pipelined_d64_edge_shapes(shape, causal, valid, dt):
+    """The software-pipelined head_dim-64 kernel against the simple MFMA kernel and the C
+    contract on lengths that are not tile multiples, tiny lengths, valid_len tails and odd
+    batch x head counts (so the workgroup remap sees counts not divisible by 8)."""
+    scale = 1.0 if dt == torch.bfloat16 else 0.4
+    q, k, v = make_qkv(shape, dt, seed=sum(shape), scale=scale)
+    a, da = _fwd(q, k, v, causal=causal, valid=valid)
+    b, db = _fwd(q, k, v, causal=causal, valid=valid, flags=_lib.FLAG_SIMPLE_SCHEDULE)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid)
+    assert np.isfinite(to_f64(a)).all()
+    assert normwise(to_f64(a), to_f64(b)) <= 4e-3
+    assert normwise(to_f64(a), c_out) <= 4e-3
+    assert normwise(to_f64(da), c_den) <= 1e-5
+
+
+def test_device_lds_limit_reported():
+    p = torch.cuda.get_device_properties(0)
+    print("device", p.name, "sharedMemPerBlock", getattr(p, "shared_memory_per_block", None),
+          "multiProcessorCount", p.multi_processor_count)
