@@ -144,14 +144,16 @@ def build_cayley_rotary_matrix(dim: int, max_seq_len: int, freqs=None, base: flo
         raise ValueError("dim must be a positive even integer")
     if max_seq_len <= 0:
         raise ValueError("max_seq_len must be a positive integer")
-    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
-    calc = torch.float64 if dtype == torch.float64 else torch.float32
     pairs = dim // 2
-    f = None
-    if freqs is not None:
-        f = torch.as_tensor(freqs, dtype=calc, device=device).contiguous()
-        if tuple(f.shape) != (pairs,):
-            raise ValueError(f"freqs must have shape ({pairs},), got {tuple(f.shape)}")
+    if freqs is not None and tuple(torch.as_tensor(freqs).shape) != (pairs,):
+        raise ValueError(f"freqs must have shape ({pairs},), got {tuple(torch.as_tensor(freqs).shape)}")
+    if device is None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("the Cayley table kernel runs on the GPU, and no HIP device is visible")
+        device = torch.device("cuda", torch.cuda.current_device())
+    device = torch.device(device)
+    calc = torch.float64 if dtype == torch.float64 else torch.float32
+    f = None if freqs is None else torch.as_tensor(freqs, dtype=calc, device=device).contiguous()
     _lib.require_device(torch.empty(0, device=device))
     c = torch.empty((max_seq_len, pairs), dtype=calc, device=device)
     s = torch.empty_like(c)

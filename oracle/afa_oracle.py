@@ -72,10 +72,12 @@ def rho8_derivative(x):
 
 
 # --------------------------------------------------------------------------- AFA forward
-def _mask(L, causal, valid_len):
-    keep = np.ones((L, L), dtype=bool)
+def _mask(Lq, Lk, causal, valid_len):
+    """Kept (query, key) pairs: key j <= query i when causal, j < valid_len when given.
+    Lk may differ from Lq (a key shard, as in src/kernels/pallas_afa.py:618-662)."""
+    keep = np.ones((Lq, Lk), dtype=bool)
     if causal:
-        keep &= np.tril(keep)
+        keep &= np.arange(Lk)[None, :] <= np.arange(Lq)[:, None]
     if valid_len is not None:
         keep[:, valid_len:] = False
     return keep
@@ -98,10 +100,10 @@ def afa_forward(q, k, v, sink_omega=0.5, causal=False, valid_len=None, rotary=No
         c, s = rotary
         q = rotate_pairs(q, c, s)
         k = rotate_pairs(k, c, s)
-    L, D = q.shape[-2], q.shape[-1]
+    D = q.shape[-1]
     scores = np.einsum("...id,...jd->...ij", q, k) / np.sqrt(D)
     w = rho8(scores)
-    w = np.where(_mask(L, causal, valid_len), w, 0.0)
+    w = np.where(_mask(q.shape[-2], k.shape[-2], causal, valid_len), w, 0.0)
     num = np.einsum("...ij,...jd->...id", w, v)
     den = w.sum(axis=-1, keepdims=True) + sink_omega
     out = num / den
@@ -136,7 +138,7 @@ def afa_backward(q, k, v, g, sink_omega=0.5, causal=False, valid_len=None):
     L, D = q.shape[-2], q.shape[-1]
     scale = 1.0 / np.sqrt(D)
     scores = np.einsum("...id,...jd->...ij", q, k) * scale
-    keep = _mask(L, causal, valid_len)
+    keep = _mask(L, L, causal, valid_len)
     w = np.where(keep, rho8(scores), 0.0)
     S = w.sum(axis=-1, keepdims=True) + sink_omega
     out = np.einsum("...ij,...jd->...id", w, v) / S

@@ -1,0 +1,111 @@
+"""The C ABI of libafa_hip.so (include/afa.h) without a GPU: the library loads, exports every
+function the header declares with the ctypes signature the binding uses, and rejects invalid
+arguments with the documented status codes before any device work (no compute calls here)."""
+import ctypes
+import math
+import os
+import re
+
+import pytest
+
+from algebraic_intelligence_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "afa.h")
+DUMMY = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w]*\s*\*?\s*([a-z_][\w]*)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from algebraic_intelligence_amd import build
+        build.build()
+    return _lib.lib()
+
+
+def test_header_declares_the_boundary():
+    names = _declared()
+    for n in ("afa_fwd", "afa_bwd", "afa_bwd_workspace_size", "asoftmax_fwd", "asoftmax_bwd",
+              "octic_fwd", "octic_bwd", "ago_build_tables", "ago_rotate", "afa_status_string",
+              "afa_last_hip_error", "afa_version"):
+        assert n in names
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    handle = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(handle, name), name
+    assert lib.afa_version() == 1
+    assert lib.afa_last_hip_error() == 0
+
+
+def test_status_strings(lib):
+    codes = [_lib.OK, _lib.ERR_NULL, _lib.ERR_DTYPE, _lib.ERR_SHAPE, _lib.ERR_HEAD_DIM, _lib.ERR_SINK,
+             _lib.ERR_VALID_LEN, _lib.ERR_EPS, _lib.ERR_ROTARY, _lib.ERR_ALIGN, _lib.ERR_WORKSPACE,
+             _lib.ERR_UNSUPPORTED, _lib.ERR_HIP]
+    texts = [lib.afa_status_string(c).decode() for c in codes]
+    assert all(texts) and len(set(texts)) == len(texts)
+    assert lib.afa_status_string(12345).decode()
+
+
+def _fwd(lib, dtype=_lib.AFA_BF16, B=1, H=1, L=64, D=64, q=DUMMY, out=DUMMY, rc=None, rs=None,
+         rot_len=0, sink=0.5, valid=0):
+    return lib.afa_fwd(dtype, B, H, L, D, q, DUMMY, DUMMY, None, out, None, rc, rs, rot_len, sink, 1,
+                       valid, 0, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=7), _lib.ERR_DTYPE),
+    (dict(dtype=-1), _lib.ERR_DTYPE),
+    (dict(q=None), _lib.ERR_NULL),
+    (dict(out=None), _lib.ERR_NULL),
+    (dict(B=0), _lib.ERR_SHAPE),
+    (dict(L=-3), _lib.ERR_SHAPE),
+    (dict(D=0), _lib.ERR_SHAPE),
+    (dict(D=192), _lib.ERR_HEAD_DIM),
+    (dict(sink=-0.5), _lib.ERR_SINK),
+    (dict(sink=math.nan), _lib.ERR_SINK),
+    (dict(sink=math.inf), _lib.ERR_SINK),
+    (dict(valid=65), _lib.ERR_VALID_LEN),
+    (dict(valid=-1), _lib.ERR_VALID_LEN),
+    (dict(rc=DUMMY), _lib.ERR_ROTARY),
+    (dict(rc=DUMMY, rs=DUMMY, rot_len=63), _lib.ERR_ROTARY),
+    (dict(rc=DUMMY, rs=DUMMY, rot_len=64, D=63), _lib.ERR_ROTARY),
+])
+def test_afa_fwd_rejects_invalid_arguments(lib, kw, code):
+    assert _fwd(lib, **kw) == code
+
+
+def test_afa_bwd_rejects_invalid_arguments(lib):
+    def bwd(dtype=_lib.AFA_BF16, D=64, g=DUMMY, sink=0.5, valid=0):
+        return lib.afa_bwd(dtype, 1, 1, 64, D, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, g, DUMMY, DUMMY, DUMMY,
+                           None, None, 0, sink, 0, valid, 0, None, 0, None)
+    assert bwd(dtype=9) == _lib.ERR_DTYPE
+    assert bwd(g=None) == _lib.ERR_NULL
+    assert bwd(D=384) == _lib.ERR_UNSUPPORTED
+    assert bwd(D=200) == _lib.ERR_HEAD_DIM
+    assert bwd(sink=-1.0) == _lib.ERR_SINK
+    assert bwd(valid=99) == _lib.ERR_VALID_LEN
+    assert lib.afa_bwd_workspace_size(_lib.AFA_BF16, 2, 16, 8192, 128) > 0
+
+
+def test_asoftmax_octic_ago_reject_invalid_arguments(lib):
+    assert lib.asoftmax_fwd(_lib.AFA_F32, 4, 8, DUMMY, DUMMY, 0.5, 0.0, None) == _lib.ERR_EPS
+    assert lib.asoftmax_fwd(_lib.AFA_F32, 4, 8, DUMMY, DUMMY, 0.5, math.inf, None) == _lib.ERR_EPS
+    assert lib.asoftmax_fwd(_lib.AFA_F32, 4, 0, DUMMY, DUMMY, 0.5, 1e-5, None) == _lib.ERR_SHAPE
+    assert lib.asoftmax_fwd(_lib.AFA_F32, 4, 8, DUMMY, DUMMY, math.nan, 1e-5, None) == _lib.ERR_SINK
+    assert lib.asoftmax_bwd(_lib.AFA_F32, 4, 8, DUMMY, None, DUMMY, 0.5, 1e-5, None) == _lib.ERR_NULL
+    assert lib.octic_fwd(11, 4, DUMMY, DUMMY, None) == _lib.ERR_DTYPE
+    assert lib.octic_bwd(_lib.AFA_F32, -1, DUMMY, DUMMY, DUMMY, None) == _lib.ERR_SHAPE
+    assert lib.ago_build_tables(_lib.AFA_BF16, 8, 16, None, 1e4, DUMMY, DUMMY, None) == _lib.ERR_DTYPE
+    assert lib.ago_build_tables(_lib.AFA_F32, 7, 16, None, 1e4, DUMMY, DUMMY, None) == _lib.ERR_SHAPE
+    assert lib.ago_rotate(_lib.AFA_F32, 1, 16, 1, 8, DUMMY, DUMMY, _lib.AFA_F32, DUMMY, DUMMY, 15,
+                          None) == _lib.ERR_ROTARY

@@ -1,0 +1,91 @@
+"""The Python call surface (algebraic_intelligence_amd) without a GPU: the reference's argument
+checks and exception types (src/kernels/pallas_afa.py:167-186, src/attention.py:60-63,155-204,
+src/primitives.py:17-21,56-59), and no silent CPU fallback for valid calls."""
+import math
+
+import pytest
+import torch
+
+import algebraic_intelligence_amd as A
+
+
+def _qkv(shape=(1, 2, 128, 64), dtype=torch.float32):
+    return [torch.zeros(shape, dtype=dtype) for _ in range(3)]
+
+
+@pytest.mark.parametrize("fn", [A.pallas_afa_forward, A.tiled_afa_forward, A.pallas_afa])
+def test_forward_argument_checks(fn):
+    q, k, v = _qkv()
+    with pytest.raises(ValueError):
+        fn(q[0], k[0], v[0])
+    with pytest.raises(ValueError):
+        fn(q, k[:, :, :64], v)
+    for bad in (-1.0, math.nan, math.inf):
+        with pytest.raises(ValueError, match="sink_omega"):
+            fn(q, k, v, sink_omega=bad)
+    with pytest.raises(ValueError):
+        fn(q, k, v, block_q=0)
+    with pytest.raises(ValueError):
+        fn(q, k, v, block_q=96)
+    with pytest.raises(ValueError, match="valid_seq_len"):
+        fn(q, k, v, valid_seq_len=0)
+    with pytest.raises(ValueError, match="valid_seq_len"):
+        fn(q, k, v, valid_seq_len=129)
+
+
+def test_head_dim_rule():
+    q, k, v = _qkv((1, 1, 128, 192))
+    with pytest.raises(ValueError, match="divisible by 128"):
+        A.pallas_afa_forward(q, k, v)
+    with pytest.raises(ValueError, match="divisible by 128"):
+        A.algebraic_flash_attention(q, k, v)
+
+
+@pytest.mark.parametrize("fn", [A.pallas_afa_forward, A.tiled_afa_forward, A.algebraic_flash_attention])
+def test_valid_calls_on_host_tensors_fail_loudly(fn):
+    """There is no CPU implementation behind the API: a valid call on host tensors raises."""
+    q, k, v = _qkv()
+    with pytest.raises(RuntimeError, match="GPU"):
+        fn(q, k, v, causal=True)
+
+
+def test_algebraic_softmax_checks():
+    x = torch.zeros(4, 8)
+    for bad in (-0.1, math.nan, math.inf):
+        with pytest.raises(ValueError, match="sink_omega"):
+            A.algebraic_softmax(x, sink_omega=bad)
+    for bad in (0.0, -1e-5, math.inf, math.nan):
+        with pytest.raises(ValueError, match="eps"):
+            A.algebraic_softmax(x, eps=bad)
+    with pytest.raises(ValueError):
+        A.algebraic_softmax(torch.zeros(4, 0))
+    with pytest.raises(TypeError):
+        A.algebraic_softmax(torch.zeros(4, 8, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="GPU"):
+        A.algebraic_softmax(x)
+
+
+def test_cayley_rotary_checks():
+    for dim in (0, -2, 7):
+        with pytest.raises(ValueError, match="dim"):
+            A.build_cayley_rotary_matrix(dim, 16)
+    with pytest.raises(ValueError, match="max_seq_len"):
+        A.build_cayley_rotary_matrix(8, 0)
+    with pytest.raises(ValueError, match="freqs"):
+        A.build_cayley_rotary_matrix(8, 16, freqs=[0.1, 0.2, 0.3])
+
+
+def test_apply_ago_rotations_checks():
+    q = torch.zeros(1, 2, 16, 8)
+    with pytest.raises(ValueError, match="shapes must match"):
+        A.apply_ago_rotations(q, torch.zeros(1, 2, 16, 6))
+    with pytest.raises(ValueError, match="even"):
+        A.apply_ago_rotations(torch.zeros(1, 2, 16, 7), torch.zeros(1, 2, 16, 7))
+    with pytest.raises(TypeError):
+        A.apply_ago_rotations(q, q, rotary_params=3.0)
+
+
+def test_flop_count_matches_definition():
+    # 4 B H D N_pairs; non-causal is the reference's 4 b h l^2 d (scripts/run_phase6_tpu.py:236)
+    assert A.afa_flops(8, 12, 4096, 64, True) == 4 * 8 * 12 * 64 * 4096 * 4097 // 2
+    assert A.afa_flops(1, 4, 256, 64, False) == 4 * 4 * 256 * 256 * 64

@@ -1,0 +1,286 @@
+"""GPU parity of the rest of the call surface: the golden fixtures through the forward, the
+analytical backward (tiled_afa_backward / pallas_afa autograd), exact_afa_reference, the padding
+front door, algebraic_softmax, octic_kernel and the Cayley rotary tables and rotation.
+
+Oracles: the 40-digit mpmath fixtures of tests/golden/, the float64 numpy oracle and the C
+contract restatement (oracle/).  Tolerances are normwise, max|y - ref| / max|ref|.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import afa_oracle as O
+from oracle import contract as C
+from tests.helpers import from_bits, make_qkv, normwise, to_bits, to_f64
+
+pytestmark = pytest.mark.gpu
+
+import algebraic_intelligence_amd as A  # noqa: E402
+
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "afa_golden.npz")
+FWD_CASES = ["fwd_plain", "fwd_causal_valid", "fwd_nosink_causal", "fwd_tail", "fwd_rotary",
+             "fwd_d64_rotary", "fwd_d128"]
+TOL = {torch.float64: 1e-12, torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 4e-3}
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _t(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(DEV)
+
+
+# ------------------------------------------------------------------------------ forward fixtures
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name", FWD_CASES)
+def test_forward_matches_golden(gold, name, dtype):
+    sink, causal, valid = gold[f"{name}_cfg"]
+    q, k, v = (_t(gold[f"{name}_{x}"], dtype) for x in "qkv")
+    L = q.shape[2]
+    rot = None
+    if f"{name}_cos" in gold:
+        rot = (torch.from_numpy(gold[f"{name}_cos"]).to(DEV), torch.from_numpy(gold[f"{name}_sin"]).to(DEV))
+    out, den = A.pallas_afa_forward(q, k, v, float(sink), bool(causal), block_q=L, block_k=L,
+                                    valid_seq_len=None if valid < 0 else int(valid),
+                                    return_denominator=True, rotary_params=rot)
+    err = normwise(to_f64(out), gold[f"{name}_out"])
+    derr = normwise(to_f64(den), gold[f"{name}_den"])
+    print(f"{name} {dtype}: out {err:.2e} den {derr:.2e}")
+    assert out.dtype == dtype
+    assert err <= TOL[dtype]
+    assert derr <= (1e-12 if dtype == torch.float64 else 1e-5 if dtype == torch.float32 else 2e-2)
+
+
+# ------------------------------------------------------------------------------ backward
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-10), (torch.float32, 2e-5)])
+def test_backward_matches_golden(gold, dtype, tol):
+    q, k, v, g = (_t(gold[f"bwd_{x}"], dtype) for x in "qkvg")
+    sink, causal, _ = gold["bwd_cfg"]
+    L = q.shape[2]
+    out, den = A.pallas_afa_forward(q, k, v, float(sink), bool(causal), block_q=L, block_k=L,
+                                    return_denominator=True)
+    grads = A.tiled_afa_backward(q, k, v, out, den, g, float(sink), bool(causal))
+    for got, key in zip(grads, ("bwd_dq", "bwd_dk", "bwd_dv")):
+        err = normwise(to_f64(got), gold[key])
+        print(key, dtype, f"{err:.2e}")
+        assert err <= tol
+
+
+@pytest.mark.parametrize("causal,valid", [(False, None), (True, None), (True, 200), (False, 77)])
+def test_backward_fp64_vs_oracle(causal, valid):
+    q, k, v = make_qkv((2, 2, 256, 32), torch.float64, seed=31)
+    g = make_qkv((2, 2, 256, 32), torch.float64, seed=32)[0]
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, causal, valid, None, 0, True)
+    dq, dk, dv = A.tiled_afa_backward(q, k, v, out, den, g, 0.5, causal, valid_seq_len=valid)
+    rq, rk, rv = O.afa_backward(to_f64(q), to_f64(k), to_f64(v), to_f64(g), 0.5, causal, valid)
+    for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+        assert normwise(to_f64(got), ref) <= 1e-10
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_low_precision(dtype):
+    """bf16 (C5's dtype, reduced length) and fp32 backward against the C contract restatement and
+    the float64 oracle (the reference gates bf16 backward at 6e-3 against fp32,
+    tests/test_pallas_afa.py:324-353)."""
+    shape = (1, 2, 256, 128)
+    q, k, v = make_qkv(shape, dtype, seed=41)
+    g = make_qkv(shape, dtype, seed=42)[0]
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, True, None, None, 0, True)
+    dq, dk, dv = A.tiled_afa_backward(q, k, v, out, den, g, 0.5, True)
+    code = {torch.bfloat16: C.DT_BF16, torch.float32: C.DT_F32}[dtype]
+    cq, ck, cv = C.afa_bwd(to_bits(q), to_bits(k), to_bits(v), to_bits(out), den.cpu().numpy(),
+                           to_bits(g), code, True)
+    rq, rk, rv = O.afa_backward(to_f64(q), to_f64(k), to_f64(v), to_f64(g), 0.5, True)
+    for name, got, cref, ref in (("dq", dq, cq, rq), ("dk", dk, ck, rk), ("dv", dv, cv, rv)):
+        e_c = normwise(to_f64(got), C.to_f32(cref, code))
+        e_r = normwise(to_f64(got), ref)
+        print(f"{dtype} {name}: vs contract {e_c:.2e} vs fp64 {e_r:.2e}")
+        assert e_c <= (6e-3 if dtype == torch.bfloat16 else 1e-5)
+        assert e_r <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
+
+
+def test_backward_with_fused_rotation():
+    """dq, dk are gradients with respect to the unrotated q, k: R^T applied to the gradients of
+    the rotated inputs."""
+    shape = (1, 2, 96, 16)
+    q, k, v = make_qkv(shape, torch.float64, seed=51)
+    g = make_qkv(shape, torch.float64, seed=52)[0]
+    c, s = O.cayley_tables(16, 96, freqs=10000.0 ** (-2.0 * np.arange(8) / 16))
+    rot = (torch.from_numpy(c).to(DEV), torch.from_numpy(s).to(DEV))
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, True, None, rot, 0, True)
+    dq, dk, dv = A.tiled_afa_backward(q, k, v, out, den, g, 0.5, True, rotary_params=rot)
+    qr, kr = O.rotate_pairs(to_f64(q), c, s), O.rotate_pairs(to_f64(k), c, s)
+    rq, rk, rv = O.afa_backward(qr, kr, to_f64(v), to_f64(g), 0.5, True)
+    assert normwise(to_f64(dq), O.rotate_pairs(rq, c, -s)) <= 1e-10
+    assert normwise(to_f64(dk), O.rotate_pairs(rk, c, -s)) <= 1e-10
+    assert normwise(to_f64(dv), rv) <= 1e-10
+
+
+def test_pallas_afa_autograd():
+    shape = (1, 2, 64, 16)
+    q, k, v = (t.requires_grad_(True) for t in make_qkv(shape, torch.float64, seed=61))
+    g = make_qkv(shape, torch.float64, seed=62)[0]
+    out = A.pallas_afa(q, k, v, 0.5, True, block_q=32, block_k=32)
+    (out * g).sum().backward()
+    rq, rk, rv = O.afa_backward(to_f64(q), to_f64(k), to_f64(v), to_f64(g), 0.5, True)
+    for got, ref in ((q.grad, rq), (k.grad, rk), (v.grad, rv)):
+        assert normwise(to_f64(got), ref) <= 1e-10
+
+
+@pytest.mark.parametrize("L", [180, 190])
+def test_flash_attention_front_door_any_length(L):
+    """Lengths that are not tile multiples (reference tests/test_pallas_afa.py:173-198)."""
+    q, k, v = (t.requires_grad_(True) for t in make_qkv((1, 2, L, 64), torch.float32, seed=L))
+    out = A.algebraic_flash_attention(q, k, v, causal=True, block_q=64, block_k=32)
+    ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, True)
+    assert out.shape == q.shape
+    assert normwise(to_f64(out), ref) <= 1e-5
+    g = torch.ones_like(out)
+    out.backward(g)
+    rq, rk, rv = O.afa_backward(to_f64(q), to_f64(k), to_f64(v), to_f64(g), 0.5, True)
+    for got, r in ((q.grad, rq), (k.grad, rk), (v.grad, rv)):
+        assert normwise(to_f64(got), r) <= 2e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_exact_afa_reference(dtype):
+    q, k, v = make_qkv((1, 2, 128, 64), dtype, seed=71)
+    out, den = A.exact_afa_with_denominator(q, k, v, 0.5, True)
+    ref, rden = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, True, return_denominator=True)
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    assert normwise(to_f64(out), ref) <= tol
+    assert normwise(to_f64(den), rden) <= tol
+    assert normwise(to_f64(A.exact_afa_reference(q, k, v, 0.5, True)), ref) <= tol
+
+
+# ------------------------------------------------------------------------------ A-Softmax / octic
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-13), (torch.float32, 2e-5), (torch.bfloat16, 1.6e-2)])
+@pytest.mark.parametrize("n", [1, 3, 7, 64])
+def test_algebraic_softmax_matches_golden(gold, n, dtype, tol):
+    sink, eps = gold[f"asm_{n}_cfg"]
+    x = _t(gold[f"asm_{n}_x"][None, :], dtype)
+    y = A.algebraic_softmax(x, float(sink), float(eps))
+    assert y.dtype == dtype
+    assert normwise(to_f64(y)[0], gold[f"asm_{n}_y"]) <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-12), (torch.float32, 2e-5)])
+def test_algebraic_softmax_forward_and_vjp(dtype, tol):
+    rng = np.random.default_rng(81)
+    x = torch.from_numpy(rng.standard_normal((3, 37, 1000)) * 3).to(dtype).to(DEV).requires_grad_(True)
+    g = torch.from_numpy(rng.standard_normal((3, 37, 1000))).to(dtype).to(DEV)
+    for sink in (0.0, 0.5, 1.0):
+        y = A.algebraic_softmax(x, sink)
+        assert normwise(to_f64(y), O.asoftmax(to_f64(x), sink)) <= tol
+        (dx,) = torch.autograd.grad(y, x, g)
+        assert normwise(to_f64(dx), O.asoftmax_vjp(to_f64(x), to_f64(g), sink)) <= tol * 10
+
+
+def test_algebraic_softmax_jacobian_at_zero():
+    eps = 1e-5
+    x = torch.zeros(1, 2, dtype=torch.float64, device=DEV, requires_grad=True)
+    J = torch.stack([torch.autograd.grad(A.algebraic_softmax(x, 0.0, eps)[0, i], x)[0][0] for i in range(2)])
+    np.testing.assert_allclose(to_f64(J) * np.sqrt(eps), [[2, -2], [-2, 2]], rtol=1e-10)
+
+
+@pytest.mark.parametrize("n", [1, 64, 4096])
+def test_algebraic_softmax_simplex_extremes(n):
+    rng = np.random.default_rng(n)
+    x = torch.from_numpy(rng.choice([-1e15, 1e15], size=(4, n))).float().to(DEV)
+    p = A.algebraic_softmax(x, 0.5)
+    assert torch.isfinite(p).all() and (p >= 0).all() and (p.sum(-1) <= 1 + 1e-5).all()
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-14), (torch.float32, 3e-6)])
+def test_octic_kernel_and_derivative(gold, dtype, tol):
+    x = _t(gold["rho8_x"], dtype).requires_grad_(True)
+    y = A.octic_kernel(x)
+    np.testing.assert_allclose(to_f64(y), gold["rho8_y"], rtol=tol)
+    (dx,) = torch.autograd.grad(y.sum(), x)
+    np.testing.assert_allclose(to_f64(dx), O.rho8_derivative(to_f64(x)), rtol=tol * 4)
+
+
+# ------------------------------------------------------------------------------ Cayley rotary
+def _f32_recurrence(w, L, base=10000.0, default=False):
+    """The table recurrence with every operation rounded in float32, in the kernel's order."""
+    one, two = np.float32(1), np.float32(2)
+    if default:
+        pairs = len(w)
+        b = np.float32(base)
+        alpha = (b * (one / np.sqrt(b)) - one) / np.float32(max(pairs - 1, 1))
+        lin = one + alpha * np.arange(pairs, dtype=np.float32)
+        w = one / (lin * lin)
+    w = np.asarray(w, dtype=np.float32)
+    w2 = w * w
+    cb, sb = (one - w2) / (one + w2), (two * w) / (one + w2)
+    c, s = np.ones_like(w), np.zeros_like(w)
+    C_, S_ = np.empty((L, len(w)), np.float32), np.empty((L, len(w)), np.float32)
+    for m in range(L):
+        C_[m], S_[m] = c, s
+        cn, sn = cb * c - sb * s, sb * c + cb * s
+        r = one / np.sqrt(cn * cn + sn * sn)
+        c, s = cn * r, sn * r
+    return C_, S_
+
+
+@pytest.mark.parametrize("name", ["cayley_default", "cayley_c3"])
+def test_cayley_tables_fp64_match_golden(gold, name):
+    cos, sin, w = gold[f"{name}_cos"], gold[f"{name}_sin"], gold[f"{name}_freqs"]
+    freqs = None if name == "cayley_default" else w
+    rot = A.build_cayley_rotary_matrix(2 * cos.shape[1], cos.shape[0], freqs=freqs, dtype=torch.float64,
+                                       device=DEV)
+    np.testing.assert_allclose(to_f64(rot.c), cos, atol=1e-13)
+    np.testing.assert_allclose(to_f64(rot.s), sin, atol=1e-13)
+
+
+@pytest.mark.parametrize("default", [False, True])
+def test_cayley_tables_fp32_bitwise_and_c3_accuracy(default):
+    D, L = 64, 4096
+    w = 10000.0 ** (-2.0 * np.arange(D // 2) / D)
+    rot = A.build_cayley_rotary_matrix(D, L, freqs=None if default else w, device=DEV)
+    c_ref, s_ref = _f32_recurrence(w, L, default=default)
+    assert np.array_equal(rot.c.cpu().numpy(), c_ref)
+    assert np.array_equal(rot.s.cpu().numpy(), s_ref)
+    c64, s64 = O.cayley_tables(D, L, freqs=None if default else w)
+    assert np.abs(to_f64(rot.c) - c64).max() < 5e-4
+    assert np.abs(to_f64(rot.s) - s64).max() < 5e-4
+
+
+@pytest.mark.parametrize("layout", ["bhld", "bld", "ld"])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-6), (torch.bfloat16, 4e-2)])
+def test_apply_ago_rotations(layout, dtype, tol):
+    shape = {"bhld": (2, 3, 40, 16), "bld": (2, 40, 16), "ld": (40, 16)}[layout]
+    rng = np.random.default_rng(91)
+    q, k = (torch.from_numpy(rng.standard_normal(shape)).to(dtype).to(DEV) for _ in range(2))
+    rot = A.build_cayley_rotary_matrix(16, 64, device=DEV)
+    qr, kr = A.apply_ago_rotations(q, k, rot)
+    c, s = to_f64(rot.c), to_f64(rot.s)  # the fp32 tables themselves are pinned above
+    seq_axis = len(shape) - 2
+    rq, rk = O.ago_apply(to_f64(q), to_f64(k), c, s, seq_axis)
+    assert qr.dtype == dtype
+    assert normwise(to_f64(qr), rq) <= tol and normwise(to_f64(kr), rk) <= tol
+
+
+def test_rotation_vjp_is_transpose():
+    x = torch.randn(2, 3, 40, 16, dtype=torch.float64, device=DEV, requires_grad=True)
+    rot = A.build_cayley_rotary_matrix(16, 40, dtype=torch.float64, device=DEV)
+    g = torch.randn_like(x)
+    y = A.rotate_tensor(x, rot.c, rot.s, 2)
+    (dx,) = torch.autograd.grad(y, x, g)
+    ref = O.rotate_pairs(to_f64(g), to_f64(rot.c), -to_f64(rot.s))
+    assert normwise(to_f64(dx), ref) <= 1e-14
+
+
+def test_fused_rotation_equals_explicit_rotation_fp32():
+    q, k, v = make_qkv((1, 2, 256, 64), torch.float32, seed=101)
+    rot = A.build_cayley_rotary_matrix(64, 256, freqs=10000.0 ** (-2.0 * np.arange(32) / 64), device=DEV)
+    fused = A.pallas_afa_forward(q, k, v, causal=True, rotary_params=rot)
+    qr, kr = A.apply_ago_rotations(q, k, rot)
+    explicit = A.pallas_afa_forward(qr, kr, v, causal=True)
+    assert normwise(to_f64(fused), to_f64(explicit)) <= 1e-6
