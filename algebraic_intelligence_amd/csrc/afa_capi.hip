@@ -22,12 +22,13 @@ size_t elem_size(int dt) { return dt == AFA_F64 ? 8 : dt == AFA_F32 ? 4 : 2; }
 size_t acc_size(int dt) { return dt == AFA_F64 ? 8 : 4; }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Cancellation error of the branch-free rho for s < 0 is at most 6e-9 per weight (absolute);
-// over n keys the relative error of out is below n * 6e-9 / sink_omega.  The fast form is
-// used only where that bound stays below 1e-3 (the bf16 rounding of P alone is 2e-3), and
-// never for fp32/fp64 inputs.
+// The branch-free rho^8 for s < 0 carries, beyond a relative error of 32 * 2^-24, an absolute
+// cancellation error below 1e-8 per weight (a float32 sweep of s in [-1e4, 0] with the
+// hardware rsqrt off by up to one ulp gives 9.3e-9).  Over n keys that adds at most
+// n * 1e-8 / sink_omega to the relative error of out, and the fast form is used only where
+// this stays below 1e-3 (the bf16 rounding of P alone is 2e-3); never for fp32/fp64 inputs.
 bool fast_rho_ok(double sink_omega, int64_t seq_len) {
-  return sink_omega > 0.0 && (double)seq_len * 6e-9 / sink_omega < 1e-3;
+  return sink_omega > 0.0 && (double)seq_len * 1e-8 / sink_omega < 1e-3;
 }
 
 struct Strides {

@@ -106,8 +106,9 @@ __device__ __forceinline__ float rho8_exact(float s) {
 
 // Branch-free evaluation rho = s + sqrt(1 + s^2) computed as fma(t, rsqrt(t), s) for both
 // signs.  Exact for s >= 0 (same expression as the reference's positive branch); for s < 0
-// the absolute error of rho^8 is below 8 rho(s)^7 |s| 2^-22 <= 6e-9, which the host only
-// accepts when sink_omega makes it negligible against the denominator (see afa_capi.cpp).
+// the cancellation adds an absolute error below 1e-8 to rho^8 (about 8 rho(s)^7 |s| 2^-22),
+// which the host accepts only when sink_omega makes it negligible against the denominator
+// (fast_rho_ok in afa_capi.hip).
 __device__ __forceinline__ float rho8_fast(float s) {
   const float t = __builtin_fmaf(s, s, 1.0f);
   const float r = __builtin_amdgcn_rsqf(t);
