@@ -1,20 +1,23 @@
 // Software-pipelined fused AFA forward for head_dim 64 (bf16 / fp16 operands, fp32 accumulate).
 //
 // Same contract as afa_fwd_mfma.hip (src/kernels/pallas_afa.py:52-151); this kernel is shaped
-// for the VALU-bound regime of head_dim 64, where each score costs ~7 VALU slots (rho^8 chain,
-// row sum, bf16 pack) against 256 MFMA FLOPs:
+// for the VALU-bound regime of head_dim 64, where each score costs ~7.5 VALU slots (rho^8
+// chain, row sum, bf16 pack) against 256 MFMA FLOPs:
 //
 //   * a wave owns 64 queries = two 32-query blocks; its key axis is cut into 32-key sub-tiles,
 //     and a "unit" is (sub-tile n, query block qb), u = 2n + qb;
 //   * unit u evaluates rho^8 of S(u) on the VALU while the MFMA pipe runs S(u+1) = K Q^T and
-//     O += V^T P(u-1); sched_group_barrier interleaves the 8 MFMAs with the ~150 VALU ops;
+//     O += V^T P(u-1); S alternates between two register sets, so no copies are made;
 //   * K tiles (Cayley-rotated on their way in) are row-major with 16 B row padding; V tiles are
 //     row-major with their two 64 B halves XOR-swizzled by (row >> 1) & 1 and are read with
 //     ds_read_tr16_b64, which returns 4 consecutive keys of one feature column per lane: two
 //     such reads form the PV MFMA's A operand in the key order of the S^T accumulator;
 //   * LDS holds 3 tiles of 64 keys: tile t+2 is stored at the end of tile t's iteration, into the
 //     buffer tile t-1 used, and a single barrier per tile orders reads and stores;
-//   * masks (causal diagonal, valid_len) are applied only on units that cross them.
+//   * masks (causal diagonal, valid_len) are applied only on units that cross them;
+//   * workgroups are dispatched heaviest query block first across all heads, with the heads of
+//     one XCD grouped together (shared L2): with 3 workgroups per slot at C3 this ordering alone
+//     removes most of the causal tail.
 #include <type_traits>
 
 #include "afa_common.h"
@@ -84,23 +87,36 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   constexpr int KSTR = D + 8;   // K row stride (elements)
   __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * KSTR];
   __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * D];
-  // staging area of the next K tile: raw rows and their Cayley table rows, filled by direct
-  // global -> LDS loads; slot c (16 B) belongs to thread chunk c
   __shared__ __attribute__((aligned(16))) unsigned short lds_kraw[KT * D];
   __shared__ __attribute__((aligned(16))) float lds_c[ROT ? KT * D / 2 : 4];
   __shared__ __attribute__((aligned(16))) float lds_s[ROT ? KT * D / 2 : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
   const int l16 = lane & 15;
   const int m16 = (lane >> 4) & 1;
 
-  const int item = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = item / a.nqb;
-  const int qblk = a.causal ? (a.nqb - 1 - item % a.nqb) : (item % a.nqb);
+  // Dispatch order -> (head, query block): heaviest query blocks of all heads first (list
+  // scheduling then approximates longest-processing-time-first), and when the head count
+  // allows, the heads of one XCD (block ids = XCD mod 8) form one contiguous group so their
+  // K/V tiles share that XCD's L2.
+  int bh, rank;
+  {
+    const int BH = a.B * a.H;
+    const int bid = blockIdx.x;
+    if ((BH & 7) == 0) {
+      const int hq = BH >> 3, j = bid >> 3;
+      bh = (bid & 7) * hq + j % hq;
+      rank = j / hq;
+    } else {
+      bh = bid % BH;
+      rank = bid / BH;
+    }
+  }
+  const int qblk = a.causal ? a.nqb - 1 - rank : rank;
   const int b = bh / a.H;
   const int h = bh % a.H;
   const int L = a.L;
@@ -113,7 +129,6 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   const int ntiles = (kend_wg + KT - 1) / KT;
   const int nsub = q0_w < L ? (kend_w + 31) / 32 : 0;  // 32-key sub-tiles of this wave
   const int U = 2 * nsub;                                // units of this wave
-
   const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
   const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
@@ -141,30 +156,47 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
     }
   }
 
-  // ---- tile staging, all by direct global -> LDS loads (no staging registers).  Thread chunk
-  // c = tid + 256 i covers key row c >> 3, 16-byte column c & 7, and a wave's loads fill one
-  // contiguous 1 KB stripe (lane slot = chunk).  V lands in its swizzled position: slot
-  // (row, physical chunk pc) receives logical chunk pc ^ (((row >> 1) & 1) << 2).  K lands raw;
-  // each thread rotates its own chunks into the K tile after its loads complete (finish_k).
-  // Rows past L read row L-1: those keys are masked, the data only has to be finite.
+  // ---- tile staging by direct global -> LDS loads.  Thread chunk c = tid + 256 i covers key
+  // row c >> 3 of the tile and 16-byte column c & 7; V lands swizzled, K raw (rotated by
+  // finish_k).  Per-thread source pointers are formed once; a tile adds t * 64 rows.
+  const int row0 = tid >> 3, c8 = tid & 7;   // chunk i = 0; chunk 1 is row0 + 32
+  const int lc0 = c8 ^ (((row0 >> 1) & 1) << 2);  // (row0 + 32) has the same swizzle
+  const unsigned short* vsrc = vp + (int64_t)row0 * a.v_l + lc0 * 8;
+  const unsigned short* ksrc = kp + (int64_t)row0 * a.k_l + c8 * 8;
+  const float* csrc = ROT ? a.rc + (int64_t)row0 * (D / 2) + c8 * 4 : nullptr;
+  const float* ssrc = ROT ? a.rs + (int64_t)row0 * (D / 2) + c8 * 4 : nullptr;
+  const int64_t v32 = 32 * a.v_l, k32 = 32 * a.k_l;
   auto issue_tile = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3, c8 = c & 7;
-      const int key = min(t * KT + row, L - 1);
-      const int stripe = (256 * i + wave * 64);  // first chunk of this wave's stripe
-      const int lc = c8 ^ (((row >> 1) & 1) << 2);
-      // (the builtin takes untyped pointers; typed ones make the host pass drop the kernel stub)
-      __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lc * 8),
-                                       (void*)&lds_v[t % NB][stripe * 8], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + c8 * 8),
-                                       (void*)&lds_kraw[stripe * 8], 16, 0, 0);
+    const int stripe0 = wave * 64, stripe1 = 256 + wave * 64;
+    if (t * KT + KT <= L) {
+      const int64_t vo = (int64_t)t * KT * a.v_l, ko = (int64_t)t * KT * a.k_l, to = (int64_t)t * KT * (D / 2);
+      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo), (void*)&lds_v[t % NB][stripe0 * 8], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo + v32), (void*)&lds_v[t % NB][stripe1 * 8], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko), (void*)&lds_kraw[stripe0 * 8], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko + k32), (void*)&lds_kraw[stripe1 * 8], 16, 0, 0);
       if constexpr (ROT) {
-        __builtin_amdgcn_global_load_lds((const void*)(a.rc + (int64_t)key * (D / 2) + c8 * 4),
-                                         (void*)&lds_c[stripe * 4], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(a.rs + (int64_t)key * (D / 2) + c8 * 4),
-                                         (void*)&lds_s[stripe * 4], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(csrc + to), (void*)&lds_c[stripe0 * 4], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(csrc + to + 32 * (D / 2)), (void*)&lds_c[stripe1 * 4], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(ssrc + to), (void*)&lds_s[stripe0 * 4], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(ssrc + to + 32 * (D / 2)), (void*)&lds_s[stripe1 * 4], 16, 0, 0);
+      }
+    } else {
+      // last, partial tile: rows past L read row L-1 (masked keys; the data only has to be finite)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = row0 + 32 * i;
+        const int key = min(t * KT + row, L - 1);
+        const int stripe = 256 * i + wave * 64;
+        __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lc0 * 8),
+                                         (void*)&lds_v[t % NB][stripe * 8], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + c8 * 8),
+                                         (void*)&lds_kraw[stripe * 8], 16, 0, 0);
+        if constexpr (ROT) {
+          __builtin_amdgcn_global_load_lds((const void*)(a.rc + (int64_t)key * (D / 2) + c8 * 4),
+                                           (void*)&lds_c[stripe * 4], 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((const void*)(a.rs + (int64_t)key * (D / 2) + c8 * 4),
+                                           (void*)&lds_s[stripe * 4], 16, 0, 0);
+        }
       }
     }
   };
@@ -173,27 +205,23 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int c = tid + 256 * i;
-      const int row = c >> 3, c8 = c & 7;
       u32x4_t kw = *(const u32x4_t*)&lds_kraw[c * 8];
       if constexpr (ROT) {
         const f32x4_t cc = *(const f32x4_t*)&lds_c[c * 4];
         const f32x4_t ss = *(const f32x4_t*)&lds_s[c * 4];
         kw = rot4<DT>(kw, cc, ss, 1.0f);
       }
-      *(u32x4_t*)&lds_k[t % NB][row * KSTR + c8 * 8] = kw;
+      *(u32x4_t*)&lds_k[t % NB][(row0 + 32 * i) * KSTR + c8 * 8] = kw;
     }
     __builtin_amdgcn_s_waitcnt(0);  // staging reads done before the next direct loads
   };
 
   // ---- per-unit fragment readers
-  // K fragment (A operand of S^T = K Q^T) of sub-tile n: key (n&1)*32 + l32 of its tile.
   auto read_kf = [&](int n, u32x4_t (&kf)[4]) {
     const unsigned short* base = &lds_k[(n >> 1) % NB][((n & 1) * 32 + l32) * KSTR + 8 * g];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) kf[kc] = *(const u32x4_t*)(base + kc * 16);
   };
-  // V^T fragments (A operand of O^T = V^T P^T) of sub-tile n: feature db*32 + l32, keys in the
-  // S^T accumulator order: half kk, elements e -> key kk*16 + (e>>2)*8 + 4g + (e&3).
   auto read_vf = [&](int n, u32x4_t (&vf)[2][2]) {
     const unsigned short* tile = lds_v[(n >> 1) % NB];
 #pragma unroll
@@ -225,13 +253,12 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
       for (int e = 0; e < 16; ++e) o[db][qb][e] = 0.f;
   float rowsum[2] = {0.f, 0.f};
 
-  // pipeline state
-  f32x16_t s_cur;       // S^T of the current unit (turned into P by it)
-  u32x4_t p_prev[2];    // packed P of the previous unit (kk halves)
-  u32x4_t kf[4];        // K fragments of the sub-tile of the next unit
-  u32x4_t vf[2][2];     // V^T fragments of the sub-tile of the previous unit
+  // pipeline state; S(u) lives in sA for odd u, in sB for even u
+  f32x16_t sA, sB;
+  u32x4_t p_prev[2];
+  u32x4_t kf[4];
+  u32x4_t vf[2][2];
 
-  // ---- prologue: tiles 0 and 1 into LDS
   if (ntiles > 0) {
     issue_tile(0);
     finish_k(0);
@@ -242,10 +269,6 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   }
   __syncthreads();
 
-  auto rho16 = [&](float (&p)[16]) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = EXACT ? rho8_exact(s_cur[r]) : rho8_fast(s_cur[r]);
-  };
   auto mask16 = [&](float (&p)[16], int u) {
     const int key0 = (u >> 1) * 32;
     const int qlo = q0_w + (u & 1) * 32;
@@ -267,106 +290,86 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
       for (int e = 0; e < 4; ++e) p_prev[kk][e] = Elem<DT>::pack(p[kk * 8 + 2 * e], p[kk * 8 + 2 * e + 1]);
   };
 
-  // ---- unit 0 (prologue): S(0), P(0), S(1); fragments K(1), V(0)
+  // ---- unit 0: S(0), P(0), S(1) -> sA; fragments K(1), V(0)
   if (U > 0) {
     read_kf(0, kf);
+    f32x16_t s0;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s_cur[e] = 0.f;
+    for (int e = 0; e < 16; ++e) s0[e] = 0.f;
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) s_cur = mma<DT>(kf[kc], qf[0][kc], s_cur);
-    f32x16_t s_nxt;
+    for (int kc = 0; kc < 4; ++kc) s0 = mma<DT>(kf[kc], qf[0][kc], s0);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s_nxt[e] = 0.f;
+    for (int e = 0; e < 16; ++e) sA[e] = 0.f;
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) s_nxt = mma<DT>(kf[kc], qf[1][kc], s_nxt);
+    for (int kc = 0; kc < 4; ++kc) sA = mma<DT>(kf[kc], qf[1][kc], sA);
     float p[16];
-    rho16(p);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = EXACT ? rho8_exact(s0[r]) : rho8_fast(s0[r]);
     mask16(p, 0);
     finish_p(p, 0);
-    s_cur = s_nxt;
     read_kf(1, kf);
     read_vf(0, vf);
   }
 
-  // Unit u = 2n + QB (QB compile-time): P(u) from s_cur; S(u+1) and PV(u-1) on the MFMA pipe,
+  // Unit u = 2n + QB: P(u) from scur = S(u); S(u+1) into snxt and PV(u-1) on the MFMA pipe,
   // interleaved with the rho^8 VALU; even units then read the fragments of sub-tiles n+1 (K)
-  // and n (V).  The last two units of a wave take the guarded tail path.
-  auto unit = [&](int u, auto qb_tag) {
+  // and n (V).  Units past the wave's last one are skipped; masks apply only where needed.
+  auto unit = [&](int u, f32x16_t& scur, f32x16_t& snxt, auto qb_tag) {
     constexpr int QB = decltype(qb_tag)::value;
-    constexpr int NQ = QB ^ 1;   // query block of unit u+1
-    constexpr int PQ = QB ^ 1;   // query block of unit u-1
+    constexpr int NQ = QB ^ 1;
+    constexpr int PQ = QB ^ 1;
     if (u > U) return;
     const int n = u >> 1;
-    if (u + 1 < U) {
-      f32x16_t s_nxt;
+    // S(u+1) unconditionally (past the wave's last unit it is never used; kf holds finite data)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s_nxt[e] = 0.f;
+    for (int e = 0; e < 16; ++e) snxt[e] = 0.f;
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) s_nxt = mma<DT>(kf[kc], qf[NQ][kc], s_nxt);
+    for (int kc = 0; kc < 4; ++kc) snxt = mma<DT>(kf[kc], qf[NQ][kc], snxt);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int db = 0; db < 2; ++db) o[db][PQ] = mma<DT>(vf[db][kk], p_prev[kk], o[db][PQ]);
+      for (int db = 0; db < 2; ++db) o[db][PQ] = mma<DT>(vf[db][kk], p_prev[kk], o[db][PQ]);
+    if (u < U) {
       float p[16];
-      rho16(p);
-      if constexpr (QB == 0) {
-        read_kf(n + 1, kf);
-        read_vf(n, vf);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);    // VALU lead-in
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // ~10 VALU
-      }
-      if constexpr (QB == 0) __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // fragment reads
+      for (int r = 0; r < 16; ++r) p[r] = EXACT ? rho8_exact(scur[r]) : rho8_fast(scur[r]);
       mask16(p, u);
       finish_p(p, QB);
-      s_cur = s_nxt;
-    } else {
-      // tail: PV(u-1) always (u >= 1), P(u) when u < U
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int db = 0; db < 2; ++db) o[db][PQ] = mma<DT>(vf[db][kk], p_prev[kk], o[db][PQ]);
-      if (u < U) {
-        float p[16];
-        rho16(p);
-        mask16(p, u);
-        finish_p(p, QB);
-        if constexpr (QB == 0) read_vf(n, vf);
+      if constexpr (QB == 0) {
+        if (u + 1 < U) read_kf(n + 1, kf);
+        read_vf(n, vf);
       }
     }
   };
 
-  // Tile t+2 goes into the buffer of tile t-1, whose last reads happened before the previous
-  // barrier; it is complete and visible after this iteration's barrier, one iteration before
-  // its first read.  Iteration t runs units 4t+1 .. 4t+4 (reading tiles t and t+1).
+  // Iteration t runs units 4t+1 .. 4t+4 (reading tiles t and t+1) and stages tile t+2 into the
+  // buffer of tile t-1, whose last reads happened before the previous barrier.
   for (int t = 0; t < ntiles; ++t) {
     if (t + 2 < ntiles) issue_tile(t + 2);
-    for (int hh = 0; hh < 2; ++hh) {
-      unit(4 * t + 2 * hh + 1, std::integral_constant<int, 1>{});
-      unit(4 * t + 2 * hh + 2, std::integral_constant<int, 0>{});
-    }
+    unit(4 * t + 1, sA, sB, std::integral_constant<int, 1>{});
+    unit(4 * t + 2, sB, sA, std::integral_constant<int, 0>{});
+    unit(4 * t + 3, sA, sB, std::integral_constant<int, 1>{});
+    unit(4 * t + 4, sB, sA, std::integral_constant<int, 0>{});
     if (t + 2 < ntiles) finish_k(t + 2);
     __syncthreads();
   }
 
-  // ---- epilogue
+  // ---- epilogue: one IEEE division per row, then products
   unsigned short* op = (unsigned short*)a.out + b * a.o_b + h * a.o_h;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const float tot = rowsum[qb] + __shfl_xor(rowsum[qb], 32) + a.omega;
     const int qi = q0_w + qb * 32 + l32;
     if (qi < L) {
+      const float inv = 1.0f / tot;
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int d0 = db * 32 + r4 * 8 + 4 * g;
           u32x2_t w;
-          w[0] = Elem<DT>::pack(o[db][qb][r4 * 4 + 0] / tot, o[db][qb][r4 * 4 + 1] / tot);
-          w[1] = Elem<DT>::pack(o[db][qb][r4 * 4 + 2] / tot, o[db][qb][r4 * 4 + 3] / tot);
+          w[0] = Elem<DT>::pack(o[db][qb][r4 * 4 + 0] * inv, o[db][qb][r4 * 4 + 1] * inv);
+          w[1] = Elem<DT>::pack(o[db][qb][r4 * 4 + 2] * inv, o[db][qb][r4 * 4 + 3] * inv);
           *(u32x2_t*)(op + (int64_t)qi * a.o_l + d0) = w;
         }
       }
