@@ -2,6 +2,7 @@
 // reference's ValueError checks, path selection, and kernel dispatch.
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "../../include/afa.h"
 #include "afa_launch.h"
@@ -27,6 +28,28 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // hardware rsqrt off by up to one ulp gives 9.3e-9).  Over n keys that adds at most
 // n * 1e-8 / sink_omega to the relative error of out, and the fast form is used only where
 // this stays below 1e-3 (the bf16 rounding of P alone is 2e-3); never for fp32/fp64 inputs.
+// Stream-ordered scratch from the current device's default memory pool.  The pool's release
+// threshold is raised once per device so that memory freed by one call is reused by the next
+// instead of being unmapped at every synchronisation.  Returns nullptr on failure.
+void* scratch_alloc(size_t bytes, hipStream_t s) {
+  static std::once_flag once[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::call_once(once[dev], [dev]() {
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+      uint64_t keep = UINT64_MAX;
+      (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    }
+  });
+  void* p = nullptr;
+  if (hipMallocAsync(&p, bytes, s) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return p;
+}
+
 bool fast_rho_ok(double sink_omega, int64_t seq_len) {
   return sink_omega > 0.0 && (double)seq_len * 1e-8 / sink_omega < 1e-3;
 }
@@ -126,8 +149,19 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     a.w_unscale = 1.0f;
     const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, vlen);
     if (head_dim == 64 && !(flags & AFA_FLAG_SIMPLE_SCHEDULE)) {
-      a.nqb = (int)((seq_len + 255) / 256);
-      return hip_status(afa::d64_fwd_launch(dtype, a, exact, s));
+      afa::FwdArgs b = a;
+      b.nqb = (int)((seq_len + 255) / 256);
+      void* krot = nullptr;
+      if (rot_cos != nullptr) krot = scratch_alloc(afa::d64_krot_bytes(b), s);
+      // without scratch for the rotated k, the single fused kernel below rotates at tile load
+      if (rot_cos == nullptr || krot != nullptr) {
+        hipError_t e = afa::d64_fwd_launch(dtype, b, exact, krot, s);
+        if (krot != nullptr) {
+          hipError_t e2 = hipFreeAsync(krot, s);
+          if (e == hipSuccess) e = e2;
+        }
+        return hip_status(e);
+      }
     }
     return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
   }

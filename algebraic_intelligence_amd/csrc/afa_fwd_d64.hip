@@ -8,16 +8,19 @@
 //     and a "unit" is (sub-tile n, query block qb), u = 2n + qb;
 //   * unit u evaluates rho^8 of S(u) on the VALU while the MFMA pipe runs S(u+1) = K Q^T and
 //     O += V^T P(u-1); S alternates between two register sets, so no copies are made;
-//   * K tiles (Cayley-rotated on their way in) are row-major with 16 B row padding; V tiles are
-//     row-major with their two 64 B halves XOR-swizzled by (row >> 1) & 1 and are read with
-//     ds_read_tr16_b64, which returns 4 consecutive keys of one feature column per lane: two
-//     such reads form the PV MFMA's A operand in the key order of the S^T accumulator;
-//   * LDS holds 3 tiles of 64 keys: tile t+2 is stored at the end of tile t's iteration, into the
-//     buffer tile t-1 used, and a single barrier per tile orders reads and stores;
+//   * K and V tiles reach LDS by direct global -> LDS loads with no register or VALU work: rows
+//     of 128 B with XOR-swizzled 16-byte chunks, K read as 32-row fragments, V with
+//     ds_read_tr16_b64, which returns 4 consecutive keys of one feature column per lane (two
+//     such reads form the PV MFMA's A operand in the key order of the S^T accumulator);
+//   * LDS is a ring of 4 tiles of 64 keys: iteration t computes on tiles t and t+1, loads tile
+//     t+3 and waits only for its own loads of tile t+2; one barrier per tile;
+//   * the Cayley rotation (AGO) of q is applied when a wave loads its queries; k is rotated
+//     once per call by afa_krot_kernel (each K tile is read by up to L/256 query blocks, so
+//     rotating it at every tile load would repeat the work that many times); both use the
+//     same fp32 arithmetic and a single rounding to the element type;
 //   * masks (causal diagonal, valid_len) are applied only on units that cross them;
 //   * workgroups are dispatched heaviest query block first across all heads, with the heads of
-//     one XCD grouped together (shared L2): with 3 workgroups per slot at C3 this ordering alone
-//     removes most of the causal tail.
+//     one XCD grouped together (shared L2).
 #include <type_traits>
 
 #include "afa_common.h"
@@ -78,18 +81,46 @@ __device__ __forceinline__ float tree16(const float (&p)[16]) {
 
 }  // namespace
 
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9: vmcnt [3:0] and [15:14]; expcnt and
+// lgkmcnt at their no-wait maxima).
+__host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// Cayley rotation of K, once per call: y (contiguous B, H, L, 64) = rotate(x) in fp32 with the
+// (L, 32) fp32 tables, rounded once to the element type -- the values the fused loader would
+// produce (rot4 with scale 1).  Grid (ceil(L / 64), B * H); each thread rotates 2 of the 8
+// 16-byte chunks of one key row (rows r and r + 32 of a 64-row block).
+template <int DT>
+__global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y) {
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh % a.H;
+  const int ch = threadIdx.x & 7;
+  const unsigned short* xb = (const unsigned short*)a.k + b * a.k_b + h * a.k_h + ch * 8;
+  unsigned short* yb = y + (int64_t)bh * a.L * 64 + ch * 8;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int l = blockIdx.x * 64 + (threadIdx.x >> 3) + 32 * i;
+    if (l < a.L) {
+      const u32x4_t w = *(const u32x4_t*)(xb + (int64_t)l * a.k_l);
+      const f32x4_t cc = *(const f32x4_t*)(a.rc + l * 32 + ch * 4);
+      const f32x4_t ss = *(const f32x4_t*)(a.rs + l * 32 + ch * 4);
+      *(u32x4_t*)(yb + (int64_t)l * 64) = rot4<DT>(w, cc, ss, 1.0f);
+    }
+  }
+}
+
 template <int DT, bool EXACT, bool ROT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void afa_fwd_d64_kernel(const FwdArgs a) {
   constexpr int D = 64;
   constexpr int KT = 64;        // keys per LDS tile
-  constexpr int NB = 3;         // LDS tile buffers
-  constexpr int KSTR = D + 8;   // K row stride (elements)
-  __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * KSTR];
+  constexpr int NB = 4;         // LDS tile buffers (a ring: tile t in buffer t & 3)
+  constexpr int LOADS = 4;      // direct loads per thread per tile (2 K + 2 V chunks)
+  // K and V tiles are row-major, 128 B per key row, 16-byte chunks XOR-swizzled: K chunk
+  // c of row r sits at c ^ (r & 7) (conflict-free 32-row fragment reads), V chunk c at
+  // c ^ (((r >> 1) & 1) << 2) (conflict-free ds_read_tr16_b64 of 4-key column slices).
+  __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * D];
   __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * D];
-  __shared__ __attribute__((aligned(16))) unsigned short lds_kraw[KT * D];
-  __shared__ __attribute__((aligned(16))) float lds_c[ROT ? KT * D / 2 : 4];
-  __shared__ __attribute__((aligned(16))) float lds_s[ROT ? KT * D / 2 : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -157,73 +188,45 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   }
 
   // ---- tile staging by direct global -> LDS loads.  Thread chunk c = tid + 256 i covers key
-  // row c >> 3 of the tile and 16-byte column c & 7; V lands swizzled, K raw (rotated by
-  // finish_k).  Per-thread source pointers are formed once; a tile adds t * 64 rows.
-  const int row0 = tid >> 3, c8 = tid & 7;   // chunk i = 0; chunk 1 is row0 + 32
-  const int lc0 = c8 ^ (((row0 >> 1) & 1) << 2);  // (row0 + 32) has the same swizzle
-  const unsigned short* vsrc = vp + (int64_t)row0 * a.v_l + lc0 * 8;
-  const unsigned short* ksrc = kp + (int64_t)row0 * a.k_l + c8 * 8;
-  const float* csrc = ROT ? a.rc + (int64_t)row0 * (D / 2) + c8 * 4 : nullptr;
-  const float* ssrc = ROT ? a.rs + (int64_t)row0 * (D / 2) + c8 * 4 : nullptr;
+  // row c >> 3 of the tile and physical 16-byte column c & 7; it loads the logical chunk that
+  // the swizzle places there.  K arrives already Cayley-rotated (rotated once per call by
+  // afa_krot_kernel), so the tiles need no further work after their loads land.
+  const int row0 = tid >> 3, c8 = tid & 7;     // chunk 1 is row0 + 32 (same low row bits)
+  const int lcv = c8 ^ (((row0 >> 1) & 1) << 2);
+  const int lck = c8 ^ (row0 & 7);
+  const unsigned short* vsrc = vp + (int64_t)row0 * a.v_l + lcv * 8;
+  const unsigned short* ksrc = kp + (int64_t)row0 * a.k_l + lck * 8;
   const int64_t v32 = 32 * a.v_l, k32 = 32 * a.k_l;
   auto issue_tile = [&](int t) {
-    const int stripe0 = wave * 64, stripe1 = 256 + wave * 64;
+    unsigned short* vdst = &lds_v[t & (NB - 1)][wave * 512];
+    unsigned short* kdst = &lds_k[t & (NB - 1)][wave * 512];
     if (t * KT + KT <= L) {
-      const int64_t vo = (int64_t)t * KT * a.v_l, ko = (int64_t)t * KT * a.k_l, to = (int64_t)t * KT * (D / 2);
-      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo), (void*)&lds_v[t % NB][stripe0 * 8], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo + v32), (void*)&lds_v[t % NB][stripe1 * 8], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko), (void*)&lds_kraw[stripe0 * 8], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko + k32), (void*)&lds_kraw[stripe1 * 8], 16, 0, 0);
-      if constexpr (ROT) {
-        __builtin_amdgcn_global_load_lds((const void*)(csrc + to), (void*)&lds_c[stripe0 * 4], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(csrc + to + 32 * (D / 2)), (void*)&lds_c[stripe1 * 4], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(ssrc + to), (void*)&lds_s[stripe0 * 4], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(ssrc + to + 32 * (D / 2)), (void*)&lds_s[stripe1 * 4], 16, 0, 0);
-      }
+      const int64_t vo = (int64_t)t * KT * a.v_l, ko = (int64_t)t * KT * a.k_l;
+      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo), (void*)vdst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo + v32), (void*)(vdst + 2048), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko), (void*)kdst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko + k32), (void*)(kdst + 2048), 16, 0, 0);
     } else {
       // last, partial tile: rows past L read row L-1 (masked keys; the data only has to be finite)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int row = row0 + 32 * i;
-        const int key = min(t * KT + row, L - 1);
-        const int stripe = 256 * i + wave * 64;
-        __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lc0 * 8),
-                                         (void*)&lds_v[t % NB][stripe * 8], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + c8 * 8),
-                                         (void*)&lds_kraw[stripe * 8], 16, 0, 0);
-        if constexpr (ROT) {
-          __builtin_amdgcn_global_load_lds((const void*)(a.rc + (int64_t)key * (D / 2) + c8 * 4),
-                                           (void*)&lds_c[stripe * 4], 16, 0, 0);
-          __builtin_amdgcn_global_load_lds((const void*)(a.rs + (int64_t)key * (D / 2) + c8 * 4),
-                                           (void*)&lds_s[stripe * 4], 16, 0, 0);
-        }
+        const int key = min(t * KT + row0 + 32 * i, L - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lcv * 8),
+                                         (void*)(vdst + 2048 * i), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + lck * 8),
+                                         (void*)(kdst + 2048 * i), 16, 0, 0);
       }
     }
-  };
-  auto finish_k = [&](int t) {
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's direct loads have landed
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;
-      u32x4_t kw = *(const u32x4_t*)&lds_kraw[c * 8];
-      if constexpr (ROT) {
-        const f32x4_t cc = *(const f32x4_t*)&lds_c[c * 4];
-        const f32x4_t ss = *(const f32x4_t*)&lds_s[c * 4];
-        kw = rot4<DT>(kw, cc, ss, 1.0f);
-      }
-      *(u32x4_t*)&lds_k[t % NB][(row0 + 32 * i) * KSTR + c8 * 8] = kw;
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // staging reads done before the next direct loads
   };
 
   // ---- per-unit fragment readers
   auto read_kf = [&](int n, u32x4_t (&kf)[4]) {
-    const unsigned short* base = &lds_k[(n >> 1) % NB][((n & 1) * 32 + l32) * KSTR + 8 * g];
+    const unsigned short* base = &lds_k[(n >> 1) & (NB - 1)][((n & 1) * 32 + l32) * D];
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) kf[kc] = *(const u32x4_t*)(base + kc * 16);
+    for (int kc = 0; kc < 4; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & 7)) * 8));
   };
   auto read_vf = [&](int n, u32x4_t (&vf)[2][2]) {
-    const unsigned short* tile = lds_v[(n >> 1) % NB];
+    const unsigned short* tile = lds_v[(n >> 1) & (NB - 1)];
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
 #pragma unroll
@@ -259,14 +262,11 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   u32x4_t kf[4];
   u32x4_t vf[2][2];
 
-  if (ntiles > 0) {
-    issue_tile(0);
-    finish_k(0);
-  }
-  if (ntiles > 1) {
-    issue_tile(1);
-    finish_k(1);
-  }
+  // prologue: tiles 0..2 in flight; wait for 0 and 1
+  const int npro = min(ntiles, 3);
+  for (int t = 0; t < npro; ++t) issue_tile(t);
+  if (npro == 3) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
+  else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
 
   auto mask16 = [&](float (&p)[16], int u) {
@@ -342,15 +342,17 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
     }
   };
 
-  // Iteration t runs units 4t+1 .. 4t+4 (reading tiles t and t+1) and stages tile t+2 into the
-  // buffer of tile t-1, whose last reads happened before the previous barrier.
+  // Iteration t reads tiles t and t+1, issues tile t+3 into the buffer of tile t-1 (last read
+  // before the previous barrier) and waits for its own loads of tile t+2, which the barrier then
+  // publishes for iteration t+1.
   for (int t = 0; t < ntiles; ++t) {
-    if (t + 2 < ntiles) issue_tile(t + 2);
+    if (t + 3 < ntiles) issue_tile(t + 3);
     unit(4 * t + 1, sA, sB, std::integral_constant<int, 1>{});
     unit(4 * t + 2, sB, sA, std::integral_constant<int, 0>{});
     unit(4 * t + 3, sA, sB, std::integral_constant<int, 1>{});
     unit(4 * t + 4, sB, sA, std::integral_constant<int, 0>{});
-    if (t + 2 < ntiles) finish_k(t + 2);
+    if (t + 3 < ntiles) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
   }
 
@@ -384,10 +386,26 @@ static hipError_t launch_d64(const FwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream) {
+size_t d64_krot_bytes(const FwdArgs& a) { return (size_t)a.B * a.H * a.L * 64 * 2; }
+
+hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream) {
   a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
   a.w_unscale = 1.0f;
   const bool rot = a.rc != nullptr;
+  if (rot) {
+    if (krot == nullptr) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.L + 63) / 64), (unsigned)(a.B * a.H));
+    if (dtype == AFA_BF16)
+      hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+    else
+      hipLaunchKernelGGL((afa_krot_kernel<AFA_F16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    a.k = krot;
+    a.k_l = 64;
+    a.k_h = (int64_t)a.L * 64;
+    a.k_b = (int64_t)a.H * a.L * 64;
+  }
   if (dtype == AFA_BF16) {
     if (exact) return rot ? launch_d64<AFA_BF16, true, true>(a, stream) : launch_d64<AFA_BF16, true, false>(a, stream);
     return rot ? launch_d64<AFA_BF16, false, true>(a, stream) : launch_d64<AFA_BF16, false, false>(a, stream);

@@ -52,8 +52,10 @@ struct GenArgs {
 bool mfma_fwd_supported(int dtype, int head_dim);
 int mfma_fwd_queries_per_block(int head_dim);
 hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
-// Software-pipelined head_dim-64 kernel (afa_fwd_d64.hip); 256 queries per workgroup.
-hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);
+// Software-pipelined head_dim-64 kernel (afa_fwd_d64.hip); 256 queries per workgroup.  With
+// rotary tables it first rotates k into `krot` (d64_krot_bytes(a) bytes of device memory).
+size_t d64_krot_bytes(const FwdArgs& a);
+hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream);
 
 hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 hipError_t generic_bwd_launch(int dtype, const GenArgs& a, hipStream_t st);

@@ -62,8 +62,12 @@ int afa_version(void);
  * s_ij = q_i.k_j / sqrt(head_dim); keys j > i are masked when causal != 0 and keys
  * j >= valid_len when valid_len > 0.  denom (nullable) receives sum_j rho^8 + sink.
  * rot_cos/rot_sin (nullable, both or neither): Cayley rotary tables (rot_len, head_dim/2),
- * fp32 (fp64 for AFA_F64); q and k rows at position i are rotated by row i at tile load
- * (fusing _rotate_tensor, src/attention.py:142-152, as called from src/model.py:262-264).
+ * fp32 (fp64 for AFA_F64); q and k rows at position i are rotated by row i (fusing
+ * _rotate_tensor, src/attention.py:142-152, as called from src/model.py:262-264): q when the
+ * kernel loads it, k at tile load, except on the bf16/fp16 head_dim-64 path, where k is
+ * rotated once per call into batch*heads*seq_len*64 elements of stream-ordered scratch
+ * (hipMallocAsync, freed on `stream` before the call returns; if that allocation fails the
+ * fully fused kernel runs instead).  AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel.
  */
 int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
             const void* q, const void* k, const void* v, const int64_t* strides, void* out,
