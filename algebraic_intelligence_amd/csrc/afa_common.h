@@ -163,11 +163,22 @@ __device__ __forceinline__ float rho8_ref(float s) {
   return k4 * k4;
 }
 
-// Number of workgroups per XCD remapping: consecutive workgroup ids go round-robin over the
-// 8 XCDs; remap so that work items adjacent in `item` order land on the same XCD (shared L2).
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
-  if ((nblocks & 7) != 0) return bid;
-  return (bid & 7) * (nblocks >> 3) + (bid >> 3);
+// Workgroup id -> (b*h, query block) for the causal/non-causal attention grids
+// (B*H*nqb workgroups).  Dispatch order is heaviest query block first across all heads, so list
+// scheduling approximates longest-processing-time-first; block id b runs on XCD b mod 8, and
+// when the head count allows, the heads of one XCD form one contiguous group (their K/V tiles
+// share that XCD's L2).  Non-causal grids use the same order (all blocks weigh the same).
+__device__ __forceinline__ void block_item(int bid, int BH, int nqb, int causal, int& bh, int& qblk) {
+  int rank;
+  if ((BH & 7) == 0) {
+    const int hq = BH >> 3, j = bid >> 3;
+    bh = (bid & 7) * hq + j % hq;
+    rank = j / hq;
+  } else {
+    bh = bid % BH;
+    rank = bid / BH;
+  }
+  qblk = causal ? nqb - 1 - rank : rank;
 }
 
 }  // namespace afa

@@ -130,24 +130,8 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   const int l16 = lane & 15;
   const int m16 = (lane >> 4) & 1;
 
-  // Dispatch order -> (head, query block): heaviest query blocks of all heads first (list
-  // scheduling then approximates longest-processing-time-first), and when the head count
-  // allows, the heads of one XCD (block ids = XCD mod 8) form one contiguous group so their
-  // K/V tiles share that XCD's L2.
-  int bh, rank;
-  {
-    const int BH = a.B * a.H;
-    const int bid = blockIdx.x;
-    if ((BH & 7) == 0) {
-      const int hq = BH >> 3, j = bid >> 3;
-      bh = (bid & 7) * hq + j % hq;
-      rank = j / hq;
-    } else {
-      bh = bid % BH;
-      rank = bid / BH;
-    }
-  }
-  const int qblk = a.causal ? a.nqb - 1 - rank : rank;
+  int bh, qblk;
+  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
   const int b = bh / a.H;
   const int h = bh % a.H;
   const int L = a.L;

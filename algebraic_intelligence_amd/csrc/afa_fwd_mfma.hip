@@ -88,10 +88,8 @@ void afa_fwd_mfma_kernel(const FwdArgs a) {
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  const int nblocks = gridDim.x;
-  const int item = xcd_remap(blockIdx.x, nblocks);
-  const int bh = item / a.nqb;
-  const int qblk = a.causal ? (a.nqb - 1 - item % a.nqb) : (item % a.nqb);
+  int bh, qblk;
+  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
   const int b = bh / a.H;
   const int h = bh % a.H;
   const int L = a.L;

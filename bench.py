@@ -1,6 +1,11 @@
 """AFA forward benchmark on one MI355X (BASELINE.json metric, configuration C3).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload c3]
+
+--workload selects another configuration of BASELINE.json for the same JSON line (the default,
+c3, is the metric's own configuration): c2 (B=4 H=8 L=2048 D=64 bf16 causal), c4 / c4f32
+(B=32 H=4 L=1024 D=64 bf16 / fp32 causal, default Cayley parameters), c5 (B=2 H=16 L=8192
+D=128 bf16 causal forward) and c5bwd (its analytical backward, 10 B H D N_pairs FLOPs).
 
 Workload (C3): B=8, H=12, L=4096, D=64, bf16, causal, q/k Cayley-rotated in-kernel with
 Cayley parameters t_i = 10000^(-2i/D); q, k, v ~ N(0, 1) synthetic, resident in HBM.
@@ -25,6 +30,20 @@ sys.path.insert(0, ROOT)
 PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "afa_fwd_c3_bf16_traffic.json")
 METRIC = "AFA fwd TFLOP/s + % bf16 MFMA peak at L=4096 D=64 (1 GPU); x vs host CPU ref"
+PEAK_FP32_TFLOPS = 157.3
+# name -> (B, H, L, D, dtype, causal, rotary freqs: "c3" | "default" | None, backward, description)
+WORKLOADS = {
+    "c3": (8, 12, 4096, 64, "bf16", True, "c3", False,
+           "C3: AFA forward, causal, Cayley rotary fused in-kernel"),
+    "c2": (4, 8, 2048, 64, "bf16", True, None, False, "C2: AFA forward, causal"),
+    "c4": (32, 4, 1024, 64, "bf16", True, "default", False,
+           "C4: AFA forward, causal, default Cayley rotary"),
+    "c4f32": (32, 4, 1024, 64, "fp32", True, "default", False,
+              "C4 (fp32): AFA forward, causal, default Cayley rotary"),
+    "c5": (2, 16, 8192, 128, "bf16", True, None, False, "C5: AFA forward, causal, head_dim 128"),
+    "c5bwd": (2, 16, 8192, 128, "bf16", True, None, True,
+              "C5: AFA analytical backward (dq, dk, dv), causal, head_dim 128"),
+}
 
 
 def parse():
@@ -34,6 +53,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB --steps times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -103,23 +123,46 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    B, H, L, D = 8, 12, 4096, 64
+    B, H, L, D, dt_name, causal, rot_kind, backward, workload = WORKLOADS[args.workload]
+    tdt = torch.bfloat16 if dt_name == "bf16" else torch.float32
+    code = _lib.AFA_BF16 if dt_name == "bf16" else _lib.AFA_F32
     g = torch.Generator(device=dev).manual_seed(0)
-    q, k, v = (torch.randn((B, H, L, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    q, k, v = (torch.randn((B, H, L, D), generator=g, device=dev, dtype=torch.float32).to(tdt)
                for _ in range(3))
-    freqs = 10000.0 ** (-2.0 * np.arange(D // 2) / D)
-    rot = A.build_cayley_rotary_matrix(D, L, freqs=freqs, device=dev)
-    rc, rs = rot.c.contiguous(), rot.s.contiguous()
+    rot = None
+    if rot_kind is not None:
+        freqs = 10000.0 ** (-2.0 * np.arange(D // 2) / D) if rot_kind == "c3" else None
+        rot = A.build_cayley_rotary_matrix(D, L, freqs=freqs, device=dev)
+    rc = rot.c.contiguous() if rot is not None else None
+    rs = rot.s.contiguous() if rot is not None else None
     out = torch.empty_like(q)
+    den = torch.empty((B, H, L, 1), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
     lib = _lib.lib()
+    ptr = _lib.ptr
 
-    def step():
-        r = lib.afa_fwd(_lib.AFA_BF16, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), None,
-                        out.data_ptr(), None, rc.data_ptr(), rs.data_ptr(), L, 0.5, 1, 0, 0,
-                        stream.cuda_stream)
+    def fwd():
+        r = lib.afa_fwd(code, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), None,
+                        out.data_ptr(), den.data_ptr() if backward else None, ptr(rc), ptr(rs),
+                        L if rot is not None else 0, 0.5, int(causal), 0, 0, stream.cuda_stream)
         if r != 0:
             _lib.check(r, "afa_fwd")
+
+    step = fwd
+    if backward:
+        fwd()
+        gout = torch.randn((B, H, L, D), generator=g, device=dev, dtype=torch.float32).to(tdt)
+        dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+        ws_bytes = lib.afa_bwd_workspace_size(code, B, H, L, D)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+        def step():
+            r = lib.afa_bwd(code, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                            den.data_ptr(), gout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                            None, None, 0, 0.5, int(causal), 0, 0, ws.data_ptr(), ws_bytes,
+                            stream.cuda_stream)
+            if r != 0:
+                _lib.check(r, "afa_bwd")
 
     for _ in range(args.warmup):
         step()
@@ -132,13 +175,14 @@ def main():
     torch.cuda.synchronize()
     ms_total = start.elapsed_time(end)
     ms = ms_total / args.steps
-    flops = A.afa_flops(B, H, L, D, causal=True)
+    flops = A.afa_flops(B, H, L, D, causal=causal) // 4 * (10 if backward else 4)
     tflops = flops / (ms * 1e-3) / 1e12
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite output")
+    peak = PEAK_BF16_TFLOPS if dt_name == "bf16" else PEAK_FP32_TFLOPS
 
     traffic = None
-    if os.path.exists(TRAFFIC_FILE):
+    if args.workload == "c3" and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
@@ -153,16 +197,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: q,k,v ~ N(0,1) bf16, resident in HBM",
-        "config": {"workload": "C3: AFA forward, causal, Cayley rotary fused in-kernel", "batch": B,
-                   "heads": H, "seq_len": L, "head_dim": D, "sink_omega": 0.5,
-                   "flops_per_step": flops},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic},
+        "dtype": dt_name,
+        "data": f"synthetic: q,k,v ~ N(0,1) {dt_name}, resident in HBM",
+        "config": {"workload": workload, "batch": B, "heads": H, "seq_len": L, "head_dim": D,
+                   "causal": causal, "sink_omega": 0.5, "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": traffic},
     }
-    if not args.no_cpu:
+    if args.workload != "c3":
+        line["metric"] = METRIC.replace("at L=4096 D=64", f"at L={L} D={D}") + f" [{args.workload}]"
+    if not args.no_cpu and args.workload == "c3":
         line["cpu_baseline"] = cpu_baseline(q, k, v, rot, args.cpu_seconds)
         line["cpu_baseline"]["gpu_speedup"] = round(tflops / line["cpu_baseline"]["value"], 1)
     print(json.dumps(line), flush=True)
