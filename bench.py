@@ -44,6 +44,11 @@ WORKLOADS = {
     "c5bwd": (2, 16, 8192, 128, "bf16", True, None, True,
               "C5: AFA analytical backward (dq, dk, dv), causal, head_dim 128"),
 }
+# A-Softmax over the last axis of (rows, cols) scores: name -> (rows, cols, dtype, backward, description)
+SOFTMAX_WORKLOADS = {
+    "asoftmax": (96 * 2048, 2048, "bf16", False, "algebraic_softmax forward, (196608, 2048) bf16 scores"),
+    "asoftmax_bwd": (96 * 2048, 2048, "bf16", True, "algebraic_softmax VJP, (196608, 2048) bf16 scores"),
+}
 
 
 def parse():
@@ -53,7 +58,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
-    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + sorted(SOFTMAX_WORKLOADS))
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB --steps times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -104,6 +109,55 @@ def cpu_baseline(q, k, v, rot, seconds):
     }
 
 
+def softmax_bench(args, dev):
+    """HBM-bound A-Softmax row kernels: GB/s of compulsory traffic (read x [and g], write y / dx)."""
+    import torch
+
+    from algebraic_intelligence_amd import _lib
+
+    rows, cols, dt_name, backward, workload = SOFTMAX_WORKLOADS[args.workload]
+    tdt = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.randn((rows, cols), generator=g, device=dev, dtype=torch.float32) * 3).to(tdt)
+    y = torch.empty_like(x)
+    gy = torch.randn((rows, cols), generator=g, device=dev, dtype=torch.float32).to(tdt)
+    stream = torch.cuda.current_stream(dev)
+    lib = _lib.lib()
+
+    def step():
+        if backward:
+            r = lib.asoftmax_bwd(_lib.AFA_BF16, rows, cols, x.data_ptr(), gy.data_ptr(), y.data_ptr(),
+                                 0.5, 1e-5, stream.cuda_stream)
+        else:
+            r = lib.asoftmax_fwd(_lib.AFA_BF16, rows, cols, x.data_ptr(), y.data_ptr(), 0.5, 1e-5,
+                                 stream.cuda_stream)
+        if r != 0:
+            _lib.check(r, "asoftmax")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    nbytes = rows * cols * 2 * (3 if backward else 2)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": f"A-Softmax {'VJP' if backward else 'forward'} HBM GB/s [{args.workload}]",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dt_name,
+        "data": "synthetic: x ~ 3 N(0,1), g ~ N(0,1) bf16, resident in HBM",
+        "config": {"workload": workload, "rows": rows, "cols": cols, "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(gbs / 8000.0, 4), "traffic": None},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -123,6 +177,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.workload in SOFTMAX_WORKLOADS:
+        softmax_bench(args, dev)
+        return
     B, H, L, D, dt_name, causal, rot_kind, backward, workload = WORKLOADS[args.workload]
     tdt = torch.bfloat16 if dt_name == "bf16" else torch.float32
     code = _lib.AFA_BF16 if dt_name == "bf16" else _lib.AFA_F32

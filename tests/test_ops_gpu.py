@@ -182,6 +182,21 @@ def test_algebraic_softmax_forward_and_vjp(dtype, tol):
         assert normwise(to_f64(dx), O.asoftmax_vjp(to_f64(x), to_f64(g), sink)) <= tol * 10
 
 
+@pytest.mark.parametrize("shape", [(16, 2048), (8, 4096), (5, 520), (3, 8), (2, 6000)])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-5), (torch.bfloat16, 1.6e-2), (torch.float16, 4e-3)])
+def test_algebraic_softmax_row_lengths(shape, dtype, tol):
+    """Row lengths that take the register-resident row kernels (up to 4096 forward, 2048 VJP)
+    and ones that fall back to the multi-pass kernels (not a multiple of the chunk width, longer
+    rows)."""
+    rng = np.random.default_rng(shape[1])
+    x = torch.from_numpy(rng.standard_normal(shape) * 2).to(dtype).to(DEV).requires_grad_(True)
+    g = torch.from_numpy(rng.standard_normal(shape)).to(dtype).to(DEV)
+    y = A.algebraic_softmax(x, 0.5)
+    assert normwise(to_f64(y), O.asoftmax(to_f64(x), 0.5)) <= tol
+    (dx,) = torch.autograd.grad(y, x, g)
+    assert normwise(to_f64(dx), O.asoftmax_vjp(to_f64(x), to_f64(g), 0.5)) <= tol * 10
+
+
 def test_algebraic_softmax_jacobian_at_zero():
     eps = 1e-5
     x = torch.zeros(1, 2, dtype=torch.float64, device=DEV, requires_grad=True)
