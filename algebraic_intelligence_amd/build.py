@@ -40,6 +40,23 @@ def _compile(src: str, obj: str, verbose: bool) -> None:
         print(msg, flush=True)
 
 
+def duplicate_kernels(objs) -> dict:
+    """Kernels defined in more than one object, as {mangled host stub: [objects]}.
+
+    A __global__ function template instantiated in two translation units with the same mangled
+    name gets one merged host handle in the shared library, while each unit's code object
+    registers its own device function under that handle: a launch from one unit can then run
+    the other unit's kernel with the wrong grid.  Kernel names must be unique across sources."""
+    seen: dict = {}
+    for obj in objs:
+        r = subprocess.run(["nm", "--defined-only", obj], capture_output=True, text=True, check=True)
+        for line in r.stdout.splitlines():
+            parts = line.split()
+            if len(parts) == 3 and "__device_stub__" in parts[2]:
+                seen.setdefault(parts[2], []).append(os.path.basename(obj))
+    return {k: v for k, v in seen.items() if len(v) > 1}
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> str:
     os.makedirs(os.path.join(BUILD, "obj"), exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -47,6 +64,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) - 1), 8)
     with cf.ThreadPoolExecutor(jobs) as ex:
         list(ex.map(lambda so: _compile(so[0], so[1], verbose), zip(srcs, objs)))
+    dup = duplicate_kernels(objs)
+    if dup:
+        raise RuntimeError("kernels defined in more than one source: " +
+                           "; ".join(f"{k} in {', '.join(v)}" for k, v in sorted(dup.items())))
     # --no-undefined: a kernel whose host stub was not emitted must fail here, not at load time
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", *objs,
            "-o", LIB + ".tmp"]

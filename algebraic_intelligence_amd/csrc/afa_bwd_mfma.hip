@@ -1,0 +1,462 @@
+// MFMA backward of the fused AFA for bf16 / fp16 operands and head_dim 64 or 128.
+//
+// Contract of tiled_afa_backward (src/kernels/pallas_afa.py:437-522) as restated by the C
+// oracle (oracle/afa_contract.c, oracle_afa_bwd):
+//   E_i = sum_d g_id out_id;  s = (q_i . k_j) * scale;  r = rsqrt(1 + s^2);  w = rho(s)^8 / d_i;
+//   ds = 8 scale r w (g_i . v_j - E_i);  dq_i += ds_ij k_j;  dk_j += ds_ij q_i;  dv_j += w_ij g_i,
+// with ds and w rounded to the input dtype as MFMA operands and fp32 accumulation.
+//
+// Three launches, no atomics:
+//   * afa_bwd_mfma_prep_kernel: E_i and 1/d_i per row into the workspace;
+//   * afa_bwd_mfma_dq_kernel (one lane per query, like the forward): S^T = K Q^T, dP^T = V g^T on
+//     MFMA, W and dS on the VALU, dQ^T += K^T dS^T with K^T read from the same LDS tile by
+//     ds_read_tr16_b64;
+//   * afa_bwd_mfma_dkdv_kernel (one lane per key): S = Q K^T, dP = g V^T, then dV^T += g^T W and
+//     dK^T += Q^T dS, with the transposed Q / g operands read from their LDS tiles.
+// The score accumulators feed the next MFMA as B operands directly: lane (column c, group g)
+// holds the 8 contraction rows {16kk + 4g + 0..3, 16kk + 8 + 4g + 0..3}, and the transposed
+// reads return exactly those rows for the A operand.
+//
+// Tiles of 64 rows are loaded by direct global -> LDS loads into two buffers; rows are D
+// elements with 16-byte chunks XOR-swizzled by (row & 7) (conflict-free 32-row fragments).
+// 1/sqrt(D) is split into a power of two folded into the register-resident operand (exact) and,
+// for D = 128, a factor 1/sqrt(2) applied to the fp32 score (the same rounding as s * scale).
+#include <type_traits>
+
+#include "afa_common.h"
+#include "afa_launch.h"
+
+namespace afa {
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+template <int DT>
+__device__ __forceinline__ f32x16_t bmma(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (DT == AFA_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// Scale 8 packed elements by a power of two (exact).
+template <int DT>
+__device__ __forceinline__ u32x4_t bscale(u32x4_t w, float sc) {
+  u32x4_t r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r[p] = Elem<DT>::pack(Elem<DT>::lo(w[p]) * sc, Elem<DT>::hi(w[p]) * sc);
+  return r;
+}
+
+// Element offset of 16-byte chunk `c` of row `r` in a swizzled tile of D-element rows.
+template <int D>
+__device__ __forceinline__ int swz(int r, int c) {
+  return r * D + ((c ^ (r & 7)) << 3);
+}
+
+// Row fragment: 8 elements (chunk c) of row r.
+template <int D>
+__device__ __forceinline__ u32x4_t frag_row(const unsigned short* tile, int r, int c) {
+  return *(const u32x4_t*)(tile + swz<D>(r, c));
+}
+
+// Transposed fragment (A operand of X^T Y, contraction over tile rows): lane (row m of the
+// 32-column block fb, group g) gets rows r0 + {4g + 0..3, 8 + 4g + 0..3} of column
+// fb * 32 + m (kk-th 16-row half selected by r0).
+template <int D>
+__device__ __forceinline__ u32x4_t frag_tr(const unsigned short* tile, int r0, int fb, int g, int l16,
+                                           int m16) {
+  u32x4_t f;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int row = r0 + hh * 8 + 4 * g + (l16 >> 2);
+    const int col = fb * 32 + m16 * 16 + 4 * (l16 & 3);
+    const unsigned short* p = tile + swz<D>(row, col >> 3) + (col & 7);
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+    const u32x2_t w = __builtin_bit_cast(u32x2_t, v);
+    f[2 * hh] = w[0];
+    f[2 * hh + 1] = w[1];
+  }
+  return f;
+}
+
+__host__ __device__ constexpr int vm_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// rho(s)^8 and r = rsqrt(1 + s^2).  EXACT: two-branch (rho(|s|)^8, reciprocal for s < 0);
+// otherwise the branch-free form, whose cancellation for s < 0 the host bounds (fast_rho_ok).
+template <bool EXACT>
+__device__ __forceinline__ float rho8r(float s, float& r) {
+  const float a = EXACT ? __builtin_fabsf(s) : s;
+  const float t = __builtin_fmaf(a, a, 1.0f);
+  r = __builtin_amdgcn_rsqf(t);
+  const float rho = __builtin_fmaf(t, r, a);
+  const float p2 = rho * rho;
+  const float p4 = p2 * p2;
+  const float p8 = p4 * p4;
+  if constexpr (EXACT) return s < 0.0f ? __builtin_amdgcn_rcpf(p8) : p8;
+  return p8;
+}
+
+}  // namespace
+
+// E_i = sum_d g_id out_id and 1/d_i per row (8 lanes per row).
+template <int DT>
+__global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a) {
+  const int64_t rows = (int64_t)a.B * a.H * a.L;
+  const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
+  float part = 0.f;
+  if (row < rows) {
+    for (int d = sub; d < a.D; d += 8)
+      part += Elem<DT>::load(a.g, row * a.D + d) * Elem<DT>::load(a.out_in, row * a.D + d);
+  }
+  part += __shfl_xor(part, 1);
+  part += __shfl_xor(part, 2);
+  part += __shfl_xor(part, 4);
+  if (row < rows && sub == 0) {
+    ((float*)a.e_ws)[row] = part;
+    ((float*)a.e_ws)[rows + row] = 1.0f / ((const float*)a.dtot)[row];
+  }
+}
+
+// ------------------------------------------------------------------------------ dQ
+template <int DT, int D, bool EXACT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, D == 64 ? 2 : 1)))
+void afa_bwd_mfma_dq_kernel(const GenArgs a) {
+  constexpr int KT = 64;
+  constexpr int NCK = D / 8;             // 16-byte chunks per row
+  constexpr int CPT = KT * NCK / 256;    // chunks per thread per tile and tensor
+  constexpr int NKC = D / 16;
+  constexpr int NFB = D / 32;
+  constexpr float SQ = D == 64 ? 1.0f : 0.70710677f;  // score factor after the folded 1/8
+  constexpr float C8 = D == 64 ? 1.0f : 0.70710677f;  // 8 * scale
+  __shared__ __attribute__((aligned(16))) unsigned short lds_k[2][KT * D];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_v[2][KT * D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5, l16 = lane & 15, m16 = (lane >> 4) & 1;
+  const int L = a.L, vlen = a.valid_len, BH = a.B * a.H;
+  const int nqb = (L + 127) / 128;
+  int bh, qblk;
+  block_item(blockIdx.x, BH, nqb, a.causal, bh, qblk);
+  const int q0_wg = qblk * 128, q0_w = q0_wg + wave * 32;
+  const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 128)) : vlen;
+  const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
+  const int ntiles = (kend_wg + KT - 1) / KT;
+  const int nsub = q0_w < L ? (kend_w + 31) / 32 : 0;
+  const int64_t base = (int64_t)bh * L * D;
+  const unsigned short* qp = (const unsigned short*)a.q + base;
+  const unsigned short* kp = (const unsigned short*)a.k + base;
+  const unsigned short* vp = (const unsigned short*)a.v + base;
+  const unsigned short* gp = (const unsigned short*)a.g + base;
+  const int qi = q0_w + l32;
+
+  u32x4_t qf[NKC], gf[NKC];
+#pragma unroll
+  for (int kc = 0; kc < NKC; ++kc) {
+    u32x4_t z = {0u, 0u, 0u, 0u};
+    qf[kc] = z;
+    gf[kc] = z;
+    if (qi < L) {
+      qf[kc] = bscale<DT>(*(const u32x4_t*)(qp + (int64_t)qi * D + 16 * kc + 8 * g), 0.125f);
+      gf[kc] = *(const u32x4_t*)(gp + (int64_t)qi * D + 16 * kc + 8 * g);
+    }
+  }
+  const int64_t rows = (int64_t)BH * L;
+  const float ei = qi < L ? ((const float*)a.e_ws)[(int64_t)bh * L + qi] : 0.f;
+  const float invd = qi < L ? ((const float*)a.e_ws)[rows + (int64_t)bh * L + qi] : 0.f;
+
+  f32x16_t dq[NFB];
+#pragma unroll
+  for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dq[fb][e] = 0.f;
+
+  auto issue = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;               // LDS chunk slot
+      const int row = c / NCK, pc = c % NCK;
+      const int key = min(t * KT + row, L - 1);
+      const int lc = pc ^ (row & 7);
+      unsigned short* kd = &lds_k[t & 1][(256 * i + wave * 64) * 8];
+      unsigned short* vd = &lds_v[t & 1][(256 * i + wave * 64) * 8];
+      __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * D + lc * 8), (void*)kd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * D + lc * 8), (void*)vd, 16, 0, 0);
+    }
+  };
+
+  if (ntiles > 0) issue(0);
+  __builtin_amdgcn_s_waitcnt(vm_only(0));
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) issue(t + 1);
+    const unsigned short* tk = lds_k[t & 1];
+    const unsigned short* tv = lds_v[t & 1];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int n = 2 * t + sub;
+      if (n < nsub) {
+        const int rk = sub * 32 + l32;
+        f32x16_t S, P;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          S[e] = 0.f;
+          P[e] = 0.f;
+        }
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<D>(tk, rk, 2 * kc + g), qf[kc], S);
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<D>(tv, rk, 2 * kc + g), gf[kc], P);
+        const bool need_mask = (a.causal && n * 32 + 31 > q0_w) || n * 32 + 31 >= vlen || q0_w + 31 >= L;
+        float ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float s = S[r] * SQ;
+          float rr;
+          const float w = rho8r<EXACT>(s, rr) * invd;
+          ds[r] = C8 * rr * w * (P[r] - ei);
+        }
+        if (need_mask) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int j = n * 32 + (r >> 2) * 8 + 4 * g + (r & 3);
+            const bool keep = j < vlen && qi < L && (!a.causal || j <= qi);
+            ds[r] = keep ? ds[r] : 0.f;
+          }
+        }
+        u32x4_t dsp[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dsp[kk][e] = Elem<DT>::pack(ds[kk * 8 + 2 * e], ds[kk * 8 + 2 * e + 1]);
+#pragma unroll
+        for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+            dq[fb] = bmma<DT>(frag_tr<D>(tk, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dq[fb]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(vm_only(0));
+    __syncthreads();
+  }
+
+  if (qi < L) {
+    unsigned short* op = (unsigned short*)a.out + base + (int64_t)qi * D;
+#pragma unroll
+    for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        u32x2_t w;
+        w[0] = Elem<DT>::pack(dq[fb][4 * r4 + 0], dq[fb][4 * r4 + 1]);
+        w[1] = Elem<DT>::pack(dq[fb][4 * r4 + 2], dq[fb][4 * r4 + 3]);
+        *(u32x2_t*)(op + fb * 32 + r4 * 8 + 4 * g) = w;
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------ dK, dV
+template <int DT, int D, bool EXACT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, D == 64 ? 2 : 1)))
+void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
+  constexpr int QT = 64;
+  constexpr int NCK = D / 8;
+  constexpr int CPT = QT * NCK / 256;
+  constexpr int NKC = D / 16;
+  constexpr int NFB = D / 32;
+  constexpr float SQ = D == 64 ? 1.0f : 0.70710677f;
+  constexpr float C8 = D == 64 ? 1.0f : 0.70710677f;
+  __shared__ __attribute__((aligned(16))) unsigned short lds_q[2][QT * D];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_g[2][QT * D];
+  __shared__ __attribute__((aligned(16))) float lds_ei[2][2 * QT];  // E then 1/d of the tile's rows
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5, l16 = lane & 15, m16 = (lane >> 4) & 1;
+  const int L = a.L, vlen = a.valid_len, BH = a.B * a.H;
+  const int nkb = (L + 127) / 128;
+  int bh, kblk;
+  // heaviest first: for causal grids the low key blocks see the most queries
+  block_item(blockIdx.x, BH, nkb, 0, bh, kblk);
+  const int k0_wg = kblk * 128, k0_w = k0_wg + wave * 32;
+  const int kj = k0_w + l32;
+  const bool wave_live = k0_w < L && k0_w < vlen;
+  const int t0 = a.causal ? k0_wg / QT : 0;
+  const int ntiles = (L + QT - 1) / QT;
+  const int64_t base = (int64_t)bh * L * D;
+  const unsigned short* qp = (const unsigned short*)a.q + base;
+  const unsigned short* kp = (const unsigned short*)a.k + base;
+  const unsigned short* vp = (const unsigned short*)a.v + base;
+  const unsigned short* gp = (const unsigned short*)a.g + base;
+  const int64_t rows = (int64_t)BH * L;
+  const float* ep = (const float*)a.e_ws + (int64_t)bh * L;
+  const float* ip = (const float*)a.e_ws + rows + (int64_t)bh * L;
+
+  u32x4_t kf[NKC], vf[NKC];
+#pragma unroll
+  for (int kc = 0; kc < NKC; ++kc) {
+    u32x4_t z = {0u, 0u, 0u, 0u};
+    kf[kc] = z;
+    vf[kc] = z;
+    if (kj < L) {
+      kf[kc] = bscale<DT>(*(const u32x4_t*)(kp + (int64_t)kj * D + 16 * kc + 8 * g), 0.125f);
+      vf[kc] = *(const u32x4_t*)(vp + (int64_t)kj * D + 16 * kc + 8 * g);
+    }
+  }
+  f32x16_t dk[NFB], dv[NFB];
+#pragma unroll
+  for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      dk[fb][e] = 0.f;
+      dv[fb][e] = 0.f;
+    }
+
+  auto issue = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / NCK, pc = c % NCK;
+      const int qrow = min(t * QT + row, L - 1);
+      const int lc = pc ^ (row & 7);
+      unsigned short* qd = &lds_q[t & 1][(256 * i + wave * 64) * 8];
+      unsigned short* gd = &lds_g[t & 1][(256 * i + wave * 64) * 8];
+      __builtin_amdgcn_global_load_lds((const void*)(qp + (int64_t)qrow * D + lc * 8), (void*)qd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(gp + (int64_t)qrow * D + lc * 8), (void*)gd, 16, 0, 0);
+    }
+    if (wave == 0 && lane < 32) {
+      // 16 lanes of E, 16 of 1/d: 4 rows per lane (L % 4 == 0, so a chunk is either inside
+      // the sequence or past it); chunks past L re-read the last one (those rows are masked)
+      const int rr = t * QT + (lane & 15) * 4;
+      const int r0 = rr < L ? rr : L - 4;
+      const float* src = (lane < 16 ? ep : ip) + r0;
+      __builtin_amdgcn_global_load_lds((const void*)src, (void*)&lds_ei[t & 1][0], 16, 0, 0);
+    }
+  };
+
+  if (t0 < ntiles) issue(t0);
+  __builtin_amdgcn_s_waitcnt(vm_only(0));
+  __syncthreads();
+
+  for (int t = t0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) issue(t + 1);
+    const unsigned short* tq = lds_q[t & 1];
+    const unsigned short* tg = lds_g[t & 1];
+    const float* tei = lds_ei[t & 1];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int m = 2 * t + sub;                      // query sub-tile
+      const bool live = wave_live && m * 32 < L && (!a.causal || m * 32 + 31 >= k0_w);
+      if (live) {
+        const int rq = sub * 32 + l32;
+        f32x16_t S, P;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          S[e] = 0.f;
+          P[e] = 0.f;
+        }
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<D>(tq, rq, 2 * kc + g), kf[kc], S);
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<D>(tg, rq, 2 * kc + g), vf[kc], P);
+        float w[16], ds[16];
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int lr = sub * 32 + r4 * 8 + 4 * g;     // tile row of element 4 r4
+          const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
+          const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * r4 + u;
+            const float s = S[r] * SQ;
+            float rr;
+            w[r] = rho8r<EXACT>(s, rr) * i4[u];
+            ds[r] = C8 * rr * w[r] * (P[r] - e4[u]);
+          }
+        }
+        const bool need_mask = (a.causal && m * 32 < k0_w + 31) || k0_w + 31 >= vlen || m * 32 + 31 >= L;
+        if (need_mask) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int i = m * 32 + (r >> 2) * 8 + 4 * g + (r & 3);
+            const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
+            w[r] = keep ? w[r] : 0.f;
+            ds[r] = keep ? ds[r] : 0.f;
+          }
+        }
+        u32x4_t wp[2], dsp[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wp[kk][e] = Elem<DT>::pack(w[kk * 8 + 2 * e], w[kk * 8 + 2 * e + 1]);
+            dsp[kk][e] = Elem<DT>::pack(ds[kk * 8 + 2 * e], ds[kk * 8 + 2 * e + 1]);
+          }
+#pragma unroll
+        for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            dv[fb] = bmma<DT>(frag_tr<D>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
+            dk[fb] = bmma<DT>(frag_tr<D>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
+          }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(vm_only(0));
+    __syncthreads();
+  }
+
+  if (kj < L) {
+    unsigned short* kout = (unsigned short*)a.dk + base + (int64_t)kj * D;
+    unsigned short* vout = (unsigned short*)a.dv + base + (int64_t)kj * D;
+#pragma unroll
+    for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        u32x2_t wk, wv;
+        wk[0] = Elem<DT>::pack(dk[fb][4 * r4 + 0], dk[fb][4 * r4 + 1]);
+        wk[1] = Elem<DT>::pack(dk[fb][4 * r4 + 2], dk[fb][4 * r4 + 3]);
+        wv[0] = Elem<DT>::pack(dv[fb][4 * r4 + 0], dv[fb][4 * r4 + 1]);
+        wv[1] = Elem<DT>::pack(dv[fb][4 * r4 + 2], dv[fb][4 * r4 + 3]);
+        *(u32x2_t*)(kout + fb * 32 + r4 * 8 + 4 * g) = wk;
+        *(u32x2_t*)(vout + fb * 32 + r4 * 8 + 4 * g) = wv;
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------ launcher
+bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len) {
+  return (dtype == AFA_BF16 || dtype == AFA_F16) && (head_dim == 64 || head_dim == 128) && seq_len >= 4 &&
+         seq_len % 4 == 0;
+}
+
+template <int DT, int D, bool EXACT>
+static hipError_t bwd_launch(const GenArgs& a, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.H * a.L;
+  hipLaunchKernelGGL((afa_bwd_mfma_prep_kernel<DT>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, st, a);
+  const int nb = a.B * a.H * ((a.L + 127) / 128);
+  hipLaunchKernelGGL((afa_bwd_mfma_dq_kernel<DT, D, EXACT>), dim3(nb), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((afa_bwd_mfma_dkdv_kernel<DT, D, EXACT>), dim3(nb), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t bwd_launch_dt(const GenArgs& a, bool exact, hipStream_t st) {
+  if (a.D == 64) return exact ? bwd_launch<DT, 64, true>(a, st) : bwd_launch<DT, 64, false>(a, st);
+  return exact ? bwd_launch<DT, 128, true>(a, st) : bwd_launch<DT, 128, false>(a, st);
+}
+
+hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, hipStream_t st) {
+  if (dtype == AFA_BF16) return bwd_launch_dt<AFA_BF16>(a, exact, st);
+  return bwd_launch_dt<AFA_F16>(a, exact, st);
+}
+
+}  // namespace afa

@@ -187,7 +187,7 @@ size_t afa_bwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t s
                               int64_t head_dim) {
   (void)head_dim;
   if (!valid_dtype(dtype) || batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
-  return (size_t)(batch * heads * seq_len) * acc_size(dtype);
+  return (size_t)(batch * heads * seq_len) * acc_size(dtype) * 2;
 }
 
 int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
@@ -196,7 +196,6 @@ int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
             const void* rot_sin, int64_t rot_len, double sink_omega, int causal,
             int64_t valid_len, unsigned flags, void* workspace, size_t workspace_bytes,
             void* stream) {
-  (void)flags;
   if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
   if (!q || !k || !v || !out || !denom || !g || !dq || !dk || !dv) return AFA_ERR_NULL;
   if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return AFA_ERR_SHAPE;
@@ -228,7 +227,12 @@ int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   a.scale = 1.0 / std::sqrt((double)head_dim);
   if (dtype != AFA_F64) a.scale = (double)(float)a.scale;
   a.omega = sink_omega;
-  hipError_t e = afa::generic_bwd_launch(dtype, a, s);
+  const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(g) &&
+                       aligned16(dq) && aligned16(dk) && aligned16(dv) && aligned16(ws) && aligned16(denom);
+  const bool use_mfma = rot_cos == nullptr && !(flags & AFA_FLAG_GENERIC) && aligned &&
+                        afa::mfma_bwd_supported(dtype, (int)head_dim, seq_len);
+  const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, a.valid_len);
+  hipError_t e = use_mfma ? afa::mfma_bwd_launch(dtype, a, exact, s) : afa::generic_bwd_launch(dtype, a, s);
   if (owned) {
     hipError_t e2 = hipFreeAsync(ws, s);
     if (e == hipSuccess) e = e2;

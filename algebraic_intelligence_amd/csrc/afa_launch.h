@@ -58,6 +58,10 @@ size_t d64_krot_bytes(const FwdArgs& a);
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream);
 
 hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
+// MFMA backward (afa_bwd_mfma.hip): bf16/fp16, head_dim 64 or 128, seq_len a multiple of 4,
+// contiguous tensors, no rotation.  e_ws holds 2 * B*H*L floats (E, then 1/d).
+bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len);
+hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, hipStream_t st);
 hipError_t generic_bwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 
 hipError_t ago_tables_launch(int table_dtype, int pairs, int len, const void* freqs, double base,

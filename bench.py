@@ -263,6 +263,8 @@ def main():
     }
     if args.workload != "c3":
         line["metric"] = METRIC.replace("at L=4096 D=64", f"at L={L} D={D}") + f" [{args.workload}]"
+        if backward:
+            line["metric"] = line["metric"].replace("AFA fwd", "AFA bwd")
     if not args.no_cpu and args.workload == "c3":
         line["cpu_baseline"] = cpu_baseline(q, k, v, rot, args.cpu_seconds)
         line["cpu_baseline"]["gpu_speedup"] = round(tflops / line["cpu_baseline"]["value"], 1)

@@ -47,6 +47,17 @@ def test_library_exports_every_declared_symbol(lib):
     assert lib.afa_last_hip_error() == 0
 
 
+def test_kernel_names_unique_across_sources(lib):
+    """Two sources defining the same kernel instantiation share one host handle in the library,
+    and a launch can run the other source's kernel with its own grid (this is how the MFMA and
+    the generic backward once collided).  The build refuses such objects; check the current ones."""
+    from algebraic_intelligence_amd import build
+    objs = sorted(os.path.join(build.BUILD, "obj", f) for f in os.listdir(os.path.join(build.BUILD, "obj"))
+                  if f.endswith(".o"))
+    assert objs
+    assert build.duplicate_kernels(objs) == {}
+
+
 def test_status_strings(lib):
     codes = [_lib.OK, _lib.ERR_NULL, _lib.ERR_DTYPE, _lib.ERR_SHAPE, _lib.ERR_HEAD_DIM, _lib.ERR_SINK,
              _lib.ERR_VALID_LEN, _lib.ERR_EPS, _lib.ERR_ROTARY, _lib.ERR_ALIGN, _lib.ERR_WORKSPACE,

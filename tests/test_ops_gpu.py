@@ -105,6 +105,53 @@ def test_backward_low_precision(dtype):
         assert e_r <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
 
 
+def _bwd_flags(q, k, v, out, den, g, causal, valid, flags):
+    """afa_bwd through the C ABI with explicit flags (contiguous inputs)."""
+    from algebraic_intelligence_amd import _lib
+    B, H, L, D = q.shape
+    dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
+    code = _lib.dtype_code(q.dtype)
+    ws_bytes = _lib.lib().afa_bwd_workspace_size(code, B, H, L, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    rc = _lib.lib().afa_bwd(code, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                            den.data_ptr(), g.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                            None, None, 0, 0.5, int(causal), 0 if valid is None else valid, flags,
+                            ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "afa_bwd")
+    return dq, dk, dv
+
+
+@pytest.mark.parametrize("shape,causal,valid", [
+    ((1, 2, 256, 64), True, None), ((2, 3, 200, 64), False, None), ((1, 2, 1000, 64), True, 777),
+    ((1, 1, 4, 64), True, None), ((1, 2, 256, 128), True, None), ((2, 1, 392, 128), False, 300),
+    ((1, 1, 128, 128), True, 61),
+])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_mfma_backward_vs_generic_and_contract(shape, causal, valid, dt):
+    """The MFMA backward (bf16/fp16, head_dim 64/128) against the generic kernel (forced with
+    AFA_FLAG_GENERIC), the C contract restatement and the float64 oracle."""
+    from algebraic_intelligence_amd import _lib
+    scale = 1.0 if dt == torch.bfloat16 else 0.5
+    q, k, v = make_qkv(shape, dt, seed=sum(shape) + 7, scale=scale)
+    g = make_qkv(shape, dt, seed=sum(shape) + 8)[0]
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, causal, valid, None, 0, True)
+    mq, mk, mv = _bwd_flags(q, k, v, out, den, g, causal, valid, 0)
+    gq, gk, gv = _bwd_flags(q, k, v, out, den, g, causal, valid, _lib.FLAG_GENERIC)
+    code = {torch.bfloat16: C.DT_BF16, torch.float16: C.DT_F16}[dt]
+    cq, ck, cv = C.afa_bwd(to_bits(q), to_bits(k), to_bits(v), to_bits(out), den.cpu().numpy(),
+                           to_bits(g), code, causal, valid)
+    rq, rk, rv = O.afa_backward(to_f64(q), to_f64(k), to_f64(v), to_f64(g), 0.5, causal, valid)
+    for name, m, gen, c, r in (("dq", mq, gq, cq, rq), ("dk", mk, gk, ck, rk), ("dv", mv, gv, cv, rv)):
+        assert torch.isfinite(m.float()).all(), name
+        e_g = normwise(to_f64(m), to_f64(gen))
+        e_c = normwise(to_f64(m), C.to_f32(c, code))
+        e_r = normwise(to_f64(m), r)
+        print(f"{shape} causal={causal} valid={valid} {dt} {name}: vs generic {e_g:.2e} "
+              f"vs contract {e_c:.2e} vs fp64 {e_r:.2e}")
+        assert e_g <= 1e-2 and e_c <= 1e-2
+        assert e_r <= 3e-2
+
+
 def test_backward_with_fused_rotation():
     """dq, dk are gradients with respect to the unrotated q, k: R^T applied to the gradients of
     the rotated inputs."""
