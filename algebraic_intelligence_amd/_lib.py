@@ -18,7 +18,7 @@ AFA_F32, AFA_BF16, AFA_F16, AFA_F64 = 0, 1, 2, 3
 FLAG_EXACT_TAIL, FLAG_GENERIC, FLAG_EXACT_REF, FLAG_SIMPLE_SCHEDULE = 0x1, 0x2, 0x4, 0x8
 
 (OK, ERR_NULL, ERR_DTYPE, ERR_SHAPE, ERR_HEAD_DIM, ERR_SINK, ERR_VALID_LEN, ERR_EPS, ERR_ROTARY,
- ERR_ALIGN, ERR_WORKSPACE, ERR_UNSUPPORTED) = range(12)
+ ERR_ALIGN, ERR_WORKSPACE, ERR_UNSUPPORTED, ERR_GAMMA) = range(13)
 ERR_HIP = 100
 
 # Every function include/afa.h declares, with its ctypes signature.
@@ -39,6 +39,13 @@ SIGNATURES = {
     "octic_bwd": (_int, [_int, _i64, _vp, _vp, _vp, _vp]),
     "ago_build_tables": (_int, [_int, _i64, _i64, _vp, _dbl, _vp, _vp, _vp]),
     "ago_rotate": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _vp, _vp, _i64, _vp]),
+    "oace_workspace_size": (_sz, [_int, _i64, _i64, _i64, _int, _uint]),
+    "oace_linear_fwd": (_int, [_int, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _vp, _dbl, _dbl, _vp, _vp,
+                               _uint, _vp, _sz, _vp]),
+    "oace_linear_bwd": (_int, [_int, _i64, _i64, _i64, _vp, _i64, _vp, _int, _i64, _vp, _dbl, _vp, _vp, _vp, _vp,
+                               _uint, _vp, _sz, _vp]),
+    "oace_softmax_loss_fwd": (_int, [_int, _i64, _i64, _vp, _vp, _dbl, _dbl, _vp, _vp, _vp]),
+    "oace_softmax_loss_bwd": (_int, [_int, _i64, _i64, _vp, _vp, _dbl, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

@@ -1,5 +1,6 @@
 // C ABI of libafa_hip.so (declared in include/afa.h): argument validation mirroring the
 // reference's ValueError checks, path selection, and kernel dispatch.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <mutex>
@@ -91,11 +92,12 @@ const char* afa_status_string(int status) {
     case AFA_ERR_HEAD_DIM: return "head dimensions above 128 must be divisible by 128";
     case AFA_ERR_SINK: return "sink_omega must be finite and nonnegative";
     case AFA_ERR_VALID_LEN: return "valid_seq_len must be in [1, seq_len]";
-    case AFA_ERR_EPS: return "eps must be finite and positive";
+    case AFA_ERR_EPS: return "eps must be finite and positive (nonnegative for the OACE loss)";
     case AFA_ERR_ROTARY: return "rotary tables must both be given, cover seq_len rows and need an even head dimension";
     case AFA_ERR_ALIGN: return "stride or pointer alignment not supported";
     case AFA_ERR_WORKSPACE: return "workspace too small";
     case AFA_ERR_UNSUPPORTED: return "combination not supported by this build";
+    case AFA_ERR_GAMMA: return "gamma must be finite and strictly positive";
     case AFA_ERR_HIP: return "HIP runtime error";
     default: return "unknown status";
   }
@@ -295,6 +297,166 @@ int ago_rotate(int dtype, int64_t outer, int64_t seq_len, int64_t inner, int64_t
   if (dim % 2 != 0 || rot_len < seq_len) return AFA_ERR_ROTARY;
   return hip_status(afa::ago_rotate_launch(dtype, table_dtype, outer, seq_len, inner, (int)dim, x, y,
                                            rot_cos, rot_sin, (hipStream_t)stream));
+}
+
+// ------------------------------------------------------------------------------ OACE
+}  // extern "C"
+
+namespace {
+
+int oace_check(int dtype, int64_t rows, int64_t d, int64_t V, const void* h, int64_t ldh, const void* w,
+               int layout, int64_t ldw, const int64_t* targets, double eps, double gamma) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (!h || !w || !targets) return AFA_ERR_NULL;
+  if (rows <= 0 || d <= 0 || V <= 0 || rows > INT32_MAX || V > INT32_MAX || d > INT32_MAX) return AFA_ERR_SHAPE;
+  if (layout != OACE_W_DV && layout != OACE_W_VD) return AFA_ERR_SHAPE;
+  if (ldh < d || ldw < (layout == OACE_W_DV ? V : d)) return AFA_ERR_SHAPE;
+  if (!(eps >= 0.0 && eps < INFINITY)) return AFA_ERR_EPS;
+  if (!(gamma > 0.0 && gamma < INFINITY)) return AFA_ERR_GAMMA;
+  return AFA_OK;
+}
+
+afa::OaceArgs oace_args(int64_t rows, int64_t d, int64_t V, const void* h, int64_t ldh, const void* w, int layout,
+                        int64_t ldw, const int64_t* targets, double eps, double gamma) {
+  afa::OaceArgs a = {};
+  a.N = rows;
+  a.d = d;
+  a.V = V;
+  a.h = h;
+  a.ldh = ldh;
+  a.w = w;
+  a.w_layout = layout;
+  a.ldw = ldw;
+  a.targets = targets;
+  a.eps = eps;
+  a.gamma = gamma;
+  return a;
+}
+
+size_t oace_rows_bytes(int dtype, int64_t rows) {
+  return ((size_t)rows * OACE_ROW_FIELDS * acc_size(dtype) + 255) & ~(size_t)255;
+}
+
+size_t oace_path_bytes(int dtype, const afa::OaceArgs& a, bool use_mfma) {
+  if (use_mfma) return afa::oace_mfma_workspace(dtype, a);
+  return std::max(afa::oace_generic_workspace(dtype, a.N, a.d, a.V, false),
+                  afa::oace_generic_workspace(dtype, a.N, a.d, a.V, true));
+}
+
+// Workspace: [row records | path scratch]; the first part is unused when the caller passes
+// row_cache.  Size from the dimensions only, the larger of the two paths.
+size_t oace_ws_size(int dtype, const afa::OaceArgs& a) {
+  return oace_rows_bytes(dtype, a.N) + std::max(oace_path_bytes(dtype, a, false), oace_path_bytes(dtype, a, true));
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t oace_workspace_size(int dtype, int64_t rows, int64_t d_model, int64_t vocab, int w_layout, unsigned flags) {
+  (void)flags;
+  if (!valid_dtype(dtype) || rows <= 0 || d_model <= 0 || vocab <= 0) return 0;
+  const afa::OaceArgs a = oace_args(rows, d_model, vocab, nullptr, d_model, nullptr, w_layout,
+                                    w_layout == OACE_W_DV ? vocab : d_model, nullptr, 0.0, 1.0);
+  return oace_ws_size(dtype, a);
+}
+
+int oace_linear_fwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, const void* h, int64_t ldh,
+                    const void* w, int w_layout, int64_t ldw, const int64_t* targets, double eps_vocab,
+                    double gamma, void* loss, void* row_cache, unsigned flags, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  int rc = oace_check(dtype, rows, d_model, vocab, h, ldh, w, w_layout, ldw, targets, eps_vocab, gamma);
+  if (rc != AFA_OK) return rc;
+  if (!loss) return AFA_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  afa::OaceArgs a = oace_args(rows, d_model, vocab, h, ldh, w, w_layout, ldw, targets, eps_vocab, gamma);
+  a.loss = loss;
+  const size_t need = oace_ws_size(dtype, a);
+  void* ws = workspace;
+  bool owned = false;
+  if (ws == nullptr) {
+    ws = scratch_alloc(need, s);
+    if (ws == nullptr) return hip_status(hipErrorOutOfMemory);
+    owned = true;
+  } else if (workspace_bytes < need) {
+    return AFA_ERR_WORKSPACE;
+  }
+  void* recs = row_cache ? row_cache : ws;
+  void* scratch = (char*)ws + oace_rows_bytes(dtype, rows);
+  const bool mfma = !(flags & AFA_FLAG_GENERIC) && afa::oace_mfma_supported(dtype, a);
+  hipError_t e = mfma ? afa::oace_linear_fwd_mfma(dtype, a, recs, scratch, s)
+                      : afa::oace_linear_fwd_generic(dtype, a, recs, scratch, s);
+  if (owned) {
+    hipError_t e2 = hipFreeAsync(ws, s);
+    if (e == hipSuccess) e = e2;
+  }
+  return hip_status(e);
+}
+
+int oace_linear_bwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, const void* h, int64_t ldh,
+                    const void* w, int w_layout, int64_t ldw, const int64_t* targets, double gamma,
+                    const void* row_cache, const void* g_loss, void* dh, void* dw, unsigned flags, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  int rc = oace_check(dtype, rows, d_model, vocab, h, ldh, w, w_layout, ldw, targets, 0.0, gamma);
+  if (rc != AFA_OK) return rc;
+  if (!row_cache || !dh || !dw) return AFA_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  afa::OaceArgs a = oace_args(rows, d_model, vocab, h, ldh, w, w_layout, ldw, targets, 0.0, gamma);
+  a.g_loss = g_loss;
+  a.dh = dh;
+  a.dw = dw;
+  const size_t need = oace_ws_size(dtype, a);
+  void* ws = workspace;
+  bool owned = false;
+  if (ws == nullptr) {
+    ws = scratch_alloc(need, s);
+    if (ws == nullptr) return hip_status(hipErrorOutOfMemory);
+    owned = true;
+  } else if (workspace_bytes < need) {
+    return AFA_ERR_WORKSPACE;
+  }
+  void* scratch = (char*)ws + oace_rows_bytes(dtype, rows);
+  const bool mfma = !(flags & AFA_FLAG_GENERIC) && afa::oace_mfma_supported(dtype, a);
+  hipError_t e = mfma ? afa::oace_linear_bwd_mfma(dtype, a, row_cache, scratch, s)
+                      : afa::oace_linear_bwd_generic(dtype, a, row_cache, scratch, s);
+  if (owned) {
+    hipError_t e2 = hipFreeAsync(ws, s);
+    if (e == hipSuccess) e = e2;
+  }
+  return hip_status(e);
+}
+
+int oace_softmax_loss_fwd(int dtype, int64_t rows, int64_t vocab, const void* logits, const int64_t* targets,
+                          double eps, double gamma, void* loss, void* row_cache, void* stream) {
+  int rc = oace_check(dtype, rows, vocab, vocab, logits, vocab, logits, OACE_W_VD, vocab, targets, eps, gamma);
+  if (rc != AFA_OK) return rc;
+  if (!loss) return AFA_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  afa::OaceArgs a = oace_args(rows, vocab, vocab, logits, vocab, nullptr, OACE_W_VD, vocab, targets, eps, gamma);
+  a.loss = loss;
+  void* recs = row_cache;
+  bool owned = false;
+  if (recs == nullptr) {
+    recs = scratch_alloc(oace_rows_bytes(dtype, rows), s);
+    if (recs == nullptr) return hip_status(hipErrorOutOfMemory);
+    owned = true;
+  }
+  hipError_t e = afa::oace_softmax_fwd_launch(dtype, a, recs, s);
+  if (owned) {
+    hipError_t e2 = hipFreeAsync(recs, s);
+    if (e == hipSuccess) e = e2;
+  }
+  return hip_status(e);
+}
+
+int oace_softmax_loss_bwd(int dtype, int64_t rows, int64_t vocab, const void* logits, const int64_t* targets,
+                          double gamma, const void* row_cache, const void* g_loss, void* dlogits, void* stream) {
+  int rc = oace_check(dtype, rows, vocab, vocab, logits, vocab, logits, OACE_W_VD, vocab, targets, 0.0, gamma);
+  if (rc != AFA_OK) return rc;
+  if (!row_cache || !dlogits) return AFA_ERR_NULL;
+  afa::OaceArgs a = oace_args(rows, vocab, vocab, logits, vocab, nullptr, OACE_W_VD, vocab, targets, 0.0, gamma);
+  a.g_loss = g_loss;
+  return hip_status(afa::oace_softmax_bwd_launch(dtype, a, row_cache, dlogits, (hipStream_t)stream));
 }
 
 }  // extern "C"

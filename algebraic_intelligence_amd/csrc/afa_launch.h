@@ -78,4 +78,40 @@ hipError_t octic_fwd_launch(int dtype, int64_t n, const void* x, void* y, hipStr
 hipError_t octic_bwd_launch(int dtype, int64_t n, const void* x, const void* g, void* dx,
                             hipStream_t st);
 
+// ---- OACE loss head (oace.hip: generic path and row kernels; oace_mfma.hip: bf16/fp16 path).
+// Per-row record (OACE_ROW values of the calc type) cached by the forward for the backward.
+enum {
+  OACE_TAU = 0, OACE_INV_S = 1, OACE_S8 = 2, OACE_SUM_P78 = 3, OACE_PC_INV8 = 4, OACE_RADIAL = 5,
+  OACE_LOSS = 6, OACE_ROW = 8
+};
+struct OaceArgs {
+  int64_t N, d, V;
+  const void* h;  // (N, d) hidden rows, row stride ldh; the logits (N, V) for the softmax loss
+  int64_t ldh;
+  const void* w;  // vocabulary projection, element (k, v) per w_layout and ldw
+  int w_layout;
+  int64_t ldw;
+  const int64_t* targets;
+  double eps, gamma;
+  void* loss;          // calc-type scalar
+  const void* g_loss;  // backward: calc-type cotangent of the loss, nullable (= 1)
+  void* dh;            // backward: (N, d) contiguous
+  void* dw;            // backward: W's layout and ldw
+};
+size_t oace_generic_chunk_rows(int dtype, int64_t N, int64_t V);
+size_t oace_generic_workspace(int dtype, int64_t N, int64_t d, int64_t V, bool backward);
+hipError_t oace_linear_fwd_generic(int dtype, const OaceArgs& a, void* rows, void* ws, hipStream_t st);
+hipError_t oace_linear_bwd_generic(int dtype, const OaceArgs& a, const void* rows, void* ws, hipStream_t st);
+hipError_t oace_mean_launch(int dtype, const void* rows, int64_t N, void* loss, hipStream_t st);
+hipError_t oace_softmax_fwd_launch(int dtype, const OaceArgs& a, void* rows, hipStream_t st);
+hipError_t oace_softmax_bwd_launch(int dtype, const OaceArgs& a, const void* rows, void* dz, hipStream_t st);
+hipError_t oace_transpose16(const void* x, int64_t rows, int64_t cols, int64_t ldx, void* y, int64_t ldy,
+                            hipStream_t st);
+// MFMA path (oace_mfma.hip): bf16/fp16, d_model a multiple of 32, 16-byte aligned rows of h (and
+// of W^T for OACE_W_VD).
+bool oace_mfma_supported(int dtype, const OaceArgs& a);
+size_t oace_mfma_workspace(int dtype, const OaceArgs& a);
+hipError_t oace_linear_fwd_mfma(int dtype, const OaceArgs& a, void* rows, void* ws, hipStream_t st);
+hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, void* ws, hipStream_t st);
+
 }  // namespace afa

@@ -1,0 +1,506 @@
+// MFMA path of the fused Linear + OACE head for bf16 / fp16 (src/kernels/pallas_oace.py:59-269).
+//
+// The vocabulary projection is never materialised in the forward.  Two GEMM sweeps over the
+// logits z = h W, each with a fused epilogue, produce per-(vocabulary tile, row) partial sums:
+//   MODE_SQ:    sum_v z^2                                  -> tau = rsqrt(mean z^2 + eps)
+//   MODE_OCTIC: sum k8, sum rho7, sum (r x) k8, sum (r x) rho7 of x = tau z
+// which small kernels reduce in a fixed order into the row records; the row kernel also forms
+// the target logit h_n . W[:, t_n] (one d_model-long dot product per row) for rho and r x there.  The reference takes the
+// second moment from the Gram matrix W W^T; the sum of squared logits is the same quantity and
+// a second sweep costs less than the Gram product whenever rows < d_model, the case of the
+// reference's own benchmark (512 x 768).  The backward recomputes z once:
+//   MODE_DZ:    dz = tau c (r bracket - radial x), stored as the element type (rows, V padded)
+// and hands dh = dz W^T and dW = h^T dz to hipBLASLt (plain GEMMs).
+//
+// GEMM tile: z^T = W^T h^T over a 256 (vocabulary) x 128 (rows) tile per workgroup, four waves of
+// 64 x 128, each a 2 x 4 grid of 32x32x16 MFMA blocks whose accumulator lanes hold one row and 16
+// vocabulary entries, so the row reductions are in-lane.  K (d_model) advances 32 per step
+// through a 3-stage LDS ring filled by direct global -> LDS loads (64-byte rows, 16-byte chunks
+// swizzled by (row >> 1) & 3: conflict-free 32-row fragment reads), one barrier per step.  Tiles
+// of one vocabulary block are dispatched consecutively on one XCD (they share its W tile in L2).
+// W is used as W^T (vocab, d_model) with d_model contiguous: a tied embedding already is; the
+// (d_model, vocab) output head is transposed once per call into the workspace.
+#include <mutex>
+#include <type_traits>
+
+#include <hipblaslt/hipblaslt.h>
+
+#include "oace_common.h"
+
+namespace afa {
+
+namespace {
+
+constexpr int TV = 256;  // vocabulary entries per workgroup tile
+constexpr int TN = 128;  // rows per workgroup tile
+constexpr int KS = 32;   // d_model per pipeline step
+constexpr int NSTAGE = 3;
+constexpr int A_BYTES = TV * KS * 2;
+constexpr int B_BYTES = TN * KS * 2;
+constexpr int STAGE = A_BYTES + B_BYTES;
+constexpr int A_LOADS = A_BYTES / (256 * 16);  // 16-byte direct loads per thread and step
+constexpr int B_LOADS = B_BYTES / (256 * 16);
+constexpr int LOADS = A_LOADS + B_LOADS;
+constexpr int MODE_SQ = 0, MODE_OCTIC = 1, MODE_DZ = 2;
+
+struct GemmArgs {
+  const unsigned short* wt;  // (V, d), row stride ldwt
+  int64_t ldwt;
+  const unsigned short* h;  // (N, d), row stride ldh
+  int64_t ldh;
+  int N, V, d, nvt, nnt;
+  const float* rows;
+  const int64_t* targets;
+  float* part;  // MODE_SQ: [nvt][N]; MODE_OCTIC: [nvt][N][4]
+  unsigned short* dz;  // MODE_DZ: (N, ldz)
+  int64_t ldz;
+  float c0;
+  const float* g_loss;
+};
+
+template <int DT>
+__device__ __forceinline__ f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (DT == AFA_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+__host__ __device__ constexpr int vm_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// Byte offset of logical 16-byte chunk lc of row r in a tile of 64-byte rows.
+__device__ __forceinline__ int chunk_off(int r, int lc) { return r * 64 + ((lc ^ ((r >> 1) & 3)) << 4); }
+
+}  // namespace
+
+template <int DT, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void oace_mfma_gemm_kernel(const GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[NSTAGE * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+
+  // tiles of one vocabulary block run consecutively on one XCD (block b runs on XCD b mod 8)
+  const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int nt = j % a.nnt, vt = (j / a.nnt) * 8 + xcd;
+  if (vt >= a.nvt) return;
+  const int v0 = vt * TV, n0 = nt * TN;
+
+  // direct-load sources: thread slot s = 256 i + tid covers row s >> 2, physical chunk s & 3
+  const unsigned short* asrc[A_LOADS];
+  const unsigned short* bsrc[B_LOADS];
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int s = 256 * i + tid, r = s >> 2, lc = (s & 3) ^ ((r >> 1) & 3);
+    asrc[i] = a.wt + (int64_t)min(v0 + r, a.V - 1) * a.ldwt + lc * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < B_LOADS; ++i) {
+    const int s = 256 * i + tid, r = s >> 2, lc = (s & 3) ^ ((r >> 1) & 3);
+    bsrc[i] = a.h + (int64_t)min(n0 + r, a.N - 1) * a.ldh + lc * 8;
+  }
+  auto issue = [&](int t) {
+    unsigned char* st = lds + (t % NSTAGE) * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + t * KS), (void*)(st + (256 * i + wave * 64) * 16), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(bsrc[i] + t * KS), (void*)(st + A_BYTES + (256 * i + wave * 64) * 16),
+                                       16, 0, 0);
+  };
+
+  f32x16_t acc[2][4];
+#pragma unroll
+  for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[vb][nb][e] = 0.f;
+
+  const int T = a.d / KS;
+  issue(0);
+  if (T > 1) issue(1);
+  if (T > 1) __builtin_amdgcn_s_waitcnt(vm_only(LOADS));
+  else __builtin_amdgcn_s_waitcnt(vm_only(0));
+  __syncthreads();
+
+  for (int t = 0; t < T; ++t) {
+    // the buffer of step t+2 was last read in step t-1, before the previous barrier
+    if (t + 2 < T) issue(t + 2);
+    const unsigned char* st = lds + (t % NSTAGE) * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      u32x4_t af[2], bf[4];
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb) af[vb] = *(const u32x4_t*)(st + chunk_off(wave * 64 + vb * 32 + l32, 2 * kk + g));
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) bf[nb] = *(const u32x4_t*)(st + A_BYTES + chunk_off(nb * 32 + l32, 2 * kk + g));
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[vb][nb] = mma<DT>(af[vb], bf[nb], acc[vb][nb]);
+    }
+    // own loads of step t+1 complete (only those of step t+2 may remain), then publish them
+    if (t + 2 < T) __builtin_amdgcn_s_waitcnt(vm_only(LOADS));
+    else __builtin_amdgcn_s_waitcnt(vm_only(0));
+    __syncthreads();
+  }
+
+  // ---- epilogue.  Element e of acc[vb][nb]: vocabulary v = vw + 32 vb + 8 (e >> 2) + 4 g + (e & 3)
+  // (vw = v0 + 64 wave), row n = n0 + 32 nb + l32.
+  const int vw = v0 + wave * 64;
+  const bool vtail = v0 + TV > a.V;
+  float* red = (float*)lds;  // the ring is idle after the last barrier
+  if constexpr (MODE == MODE_SQ) {
+    float s[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      s[nb] = 0.f;
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float z = acc[vb][nb][e];
+          const int v = vw + 32 * vb + 8 * (e >> 2) + 4 * g + (e & 3);
+          s[nb] += (!vtail || v < a.V) ? z * z : 0.f;
+        }
+      s[nb] += __shfl_xor(s[nb], 32);
+      if (g == 0) red[wave * TN + nb * 32 + l32] = s[nb];
+    }
+    __syncthreads();
+    if (tid < TN && n0 + tid < a.N)
+      a.part[(int64_t)vt * a.N + n0 + tid] = (red[tid] + red[TN + tid]) + (red[2 * TN + tid] + red[3 * TN + tid]);
+  } else if constexpr (MODE == MODE_OCTIC) {
+    float tau[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int n = n0 + nb * 32 + l32;
+      tau[nb] = n < a.N ? a.rows[(int64_t)n * OACE_ROW + OACE_TAU] : 0.f;
+    }
+    // masks only in the last vocabulary tile (uniform branch)
+    auto sums = [&](auto masked) {
+      const int vlim = a.V - vw - 4 * g;  // entries e with 32 vb + 8 (e >> 2) + (e & 3) < vlim exist
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float x = acc[vb][nb][e] * tau[nb];
+            const Oct<float> o = octic(x);
+            const float rn = o.r * x;
+            const bool in = !decltype(masked)::value || 32 * vb + 8 * (e >> 2) + (e & 3) < vlim;
+            s[0] += in ? o.k8 : 0.f;
+            s[1] += in ? o.rho7 : 0.f;
+            s[2] += in ? rn * o.k8 : 0.f;
+            s[3] += in ? rn * o.rho7 : 0.f;
+          }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x = s[q] + __shfl_xor(s[q], 32);
+          if (g == 0) red[(wave * 4 + q) * TN + nb * 32 + l32] = x;
+        }
+        // keep the row blocks apart: interleaving their octic chains costs more registers than exist
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if (vtail) sums(std::true_type{});
+    else sums(std::false_type{});
+    __syncthreads();
+    for (int i = tid; i < TN * 4; i += 256) {
+      const int q = i / TN, nl = i % TN;
+      if (n0 + nl < a.N)
+        a.part[((int64_t)vt * a.N + n0 + nl) * 4 + q] =
+            (red[q * TN + nl] + red[(4 + q) * TN + nl]) + (red[(8 + q) * TN + nl] + red[(12 + q) * TN + nl]);
+    }
+  } else {  // MODE_DZ
+    const float gl = a.g_loss ? *a.g_loss : 1.f;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int n = n0 + nb * 32 + l32;
+      if (n >= a.N) continue;
+      const float* rec = a.rows + (int64_t)n * OACE_ROW;
+      const float tau = rec[OACE_TAU], inv_S = rec[OACE_INV_S], pc = rec[OACE_PC_INV8], radial = rec[OACE_RADIAL];
+      const float scale = rec[OACE_S8] * inv_S;
+      const float diff = rec[OACE_SUM_P78] - pc;
+      const float tc = tau * (a.c0 * gl);
+      const int64_t t = a.targets[n];
+      unsigned short* drow = a.dz + (int64_t)n * a.ldz;
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int vs = vw + 32 * vb + 8 * e4 + 4 * g;
+          float dzv[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float x = acc[vb][nb][4 * e4 + u] * tau;
+            const Oct<float> o = octic(x);
+            const float bracket = scale * o.rho7 - (vs + u == t ? pc : 0.f) - (o.k8 * inv_S) * diff;
+            dzv[u] = tc * (o.r * bracket - radial * x);
+          }
+          if (vs < a.V) {
+            u32x2_t w;
+            w[0] = Elem<DT>::pack(dzv[0], dzv[1]);
+            w[1] = Elem<DT>::pack(dzv[2], dzv[3]);
+            *(u32x2_t*)(drow + vs) = w;
+          }
+        }
+    }
+  }
+}
+
+// tau per row from the MODE_SQ partials, summed over vocabulary tiles in order.
+__global__ __launch_bounds__(256) void oace_mfma_tau_kernel(const float* part, int nvt, int N, float inv_v, float eps,
+                                                            float* rows) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  float ss = 0.f;
+  for (int t = 0; t < nvt; ++t) ss += part[(int64_t)t * N + n];
+  rows[(int64_t)n * OACE_ROW + OACE_TAU] = o_rsq<float>(ss * inv_v + eps);
+}
+
+// Row records from the MODE_OCTIC partials, one wave per row.  The target logit is the dot
+// product of the row of h with row t of W^T (fp32 accumulation of the exact element products,
+// as the GEMM); a target outside [0, V) leaves rho_t = 0 (infinite loss), as the reference.
+template <int DT>
+__global__ __launch_bounds__(256) void oace_mfma_rows_kernel(const float* part, int nvt, int N, float inv_v,
+                                                             float gamma, const unsigned short* h, int64_t ldh,
+                                                             const unsigned short* wt, int64_t ldwt, int d, int V,
+                                                             const int64_t* targets, float* rows) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int64_t t = targets[n];
+  const bool valid = t >= 0 && t < V;
+  float z = 0.f;
+  if (valid) {
+    const unsigned short* hr = h + (int64_t)n * ldh;
+    const unsigned short* wr = wt + t * ldwt;
+    for (int k = 2 * lane; k < d; k += 128) {
+      const unsigned hw = *(const unsigned*)(hr + k), ww = *(const unsigned*)(wr + k);
+      z += Elem<DT>::lo(hw) * Elem<DT>::lo(ww) + Elem<DT>::hi(hw) * Elem<DT>::hi(ww);
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) z += __shfl_xor(z, m);
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int vt = lane; vt < nvt; vt += 64)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s[q] += part[((int64_t)vt * N + n) * 4 + q];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s[q] += __shfl_xor(s[q], m);
+  if (lane == 0) {
+    float* rec = rows + (int64_t)n * OACE_ROW;
+    const float tau = rec[OACE_TAU];
+    float rho_t = 0.f, rn_t = 0.f;
+    if (valid) {
+      const float x = z * tau;
+      const Oct<float> o = octic(x);
+      rho_t = o.rho;
+      rn_t = o.r * x;
+    }
+    oace_finalize_row<float>(rec, tau, s[0], s[1], s[2], s[3], rho_t, rn_t, inv_v, gamma);
+  }
+}
+
+// ------------------------------------------------------------------------------ host side
+namespace {
+
+int64_t nvt_of(int64_t V) { return (V + TV - 1) / TV; }
+int64_t nnt_of(int64_t N) { return (N + TN - 1) / TN; }
+int64_t ldz_of(int64_t V) { return (V + 63) / 64 * 64; }
+size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+constexpr size_t BLAS_WS = (size_t)64 << 20;
+
+bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+struct Layout {
+  size_t wt, part, dz, blas, total;
+};
+Layout layout_of(const OaceArgs& a) {
+  Layout l;
+  l.wt = a.w_layout == OACE_W_DV ? al((size_t)a.V * a.d * 2) : 0;
+  l.part = al((size_t)nvt_of(a.V) * a.N * 4 * sizeof(float));
+  l.dz = al((size_t)a.N * ldz_of(a.V) * 2);
+  l.blas = BLAS_WS;
+  l.total = l.wt + std::max(l.part, l.dz + l.blas);
+  return l;
+}
+
+// W^T (V, d) with d contiguous: the caller's tied embedding, or a transposed copy in ws.
+const unsigned short* wt_of(const OaceArgs& a, void* ws, int64_t& ldwt, hipStream_t st, hipError_t& e) {
+  e = hipSuccess;
+  if (a.w_layout == OACE_W_VD) {
+    ldwt = a.ldw;
+    return (const unsigned short*)a.w;
+  }
+  ldwt = a.d;
+  e = oace_transpose16(a.w, a.d, a.V, a.ldw, ws, a.d, st);
+  return (const unsigned short*)ws;
+}
+
+GemmArgs gemm_args(const OaceArgs& a, const unsigned short* wt, int64_t ldwt) {
+  GemmArgs g = {};
+  g.wt = wt;
+  g.ldwt = ldwt;
+  g.h = (const unsigned short*)a.h;
+  g.ldh = a.ldh;
+  g.N = (int)a.N;
+  g.V = (int)a.V;
+  g.d = (int)a.d;
+  g.nvt = (int)nvt_of(a.V);
+  g.nnt = (int)nnt_of(a.N);
+  g.targets = a.targets;
+  return g;
+}
+
+template <int DT, int MODE>
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t st) {
+  const unsigned grid = (unsigned)(8 * g.nnt * ((g.nvt + 7) / 8));
+  hipLaunchKernelGGL((oace_mfma_gemm_kernel<DT, MODE>), dim3(grid), dim3(256), 0, st, g);
+  return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_gemm_dt(int dtype, const GemmArgs& g, hipStream_t st) {
+  return dtype == AFA_BF16 ? launch_gemm<AFA_BF16, MODE>(g, st) : launch_gemm<AFA_F16, MODE>(g, st);
+}
+
+// ---- hipBLASLt for the two plain GEMMs of the backward (one handle per device, created once).
+hipblasLtHandle_t blas_handle() {
+  static std::mutex m;
+  static hipblasLtHandle_t handles[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(m);
+  if (handles[dev] == nullptr && hipblasLtCreate(&handles[dev]) != HIPBLAS_STATUS_SUCCESS) handles[dev] = nullptr;
+  return handles[dev];
+}
+
+// Column-major D (m x n, ldd) = op(A) op(B), k the contraction; A stored (ta ? k x m : m x k) with
+// lda, B stored (tb ? n x k : k x n) with ldb; fp32 accumulation, element-type output.
+hipError_t blas_gemm(int dtype, bool ta, bool tb, int64_t m, int64_t n, int64_t k, const void* A, int64_t lda,
+                     const void* B, int64_t ldb, void* D, int64_t ldd, void* ws, size_t wsb, hipStream_t st) {
+  hipblasLtHandle_t h = blas_handle();
+  if (h == nullptr) return hipErrorNotInitialized;
+  const hipDataType t = dtype == AFA_BF16 ? HIP_R_16BF : HIP_R_16F;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  hipError_t err = hipErrorNotSupported;
+  const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  const uint64_t wsz = wsb;
+  hipblasLtMatmulHeuristicResult_t res[1];
+  int found = 0;
+  const float alpha = 1.f, beta = 0.f;
+  if (hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) goto done;
+  if (hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(int32_t)) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(int32_t)) != HIPBLAS_STATUS_SUCCESS)
+    goto done;
+  if (hipblasLtMatrixLayoutCreate(&la, t, ta ? k : m, ta ? m : k, lda) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&lb, t, tb ? n : k, tb ? k : n, ldb) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&ld, t, m, n, ldd) != HIPBLAS_STATUS_SUCCESS)
+    goto done;
+  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof(wsz)) !=
+          HIPBLAS_STATUS_SUCCESS)
+    goto done;
+  if (hipblasLtMatmulAlgoGetHeuristic(h, desc, la, lb, ld, ld, pref, 1, res, &found) != HIPBLAS_STATUS_SUCCESS ||
+      found < 1)
+    goto done;
+  if (hipblasLtMatmul(h, desc, &alpha, A, la, B, lb, &beta, D, ld, D, ld, &res[0].algo, ws, wsb, st) ==
+      HIPBLAS_STATUS_SUCCESS)
+    err = hipSuccess;
+done:
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  if (ld) hipblasLtMatrixLayoutDestroy(ld);
+  if (lb) hipblasLtMatrixLayoutDestroy(lb);
+  if (la) hipblasLtMatrixLayoutDestroy(la);
+  if (desc) hipblasLtMatmulDescDestroy(desc);
+  return err;
+}
+
+}  // namespace
+
+bool oace_mfma_supported(int dtype, const OaceArgs& a) {
+  if (dtype != AFA_BF16 && dtype != AFA_F16) return false;
+  if (a.d % KS != 0 || a.ldh % 8 != 0 || !al16(a.h)) return false;
+  if (a.w_layout == OACE_W_VD && (a.ldw % 8 != 0 || !al16(a.w))) return false;
+  if (a.N > (1 << 28) || a.V > (1 << 28)) return false;
+  return true;
+}
+
+size_t oace_mfma_workspace(int dtype, const OaceArgs& a) {
+  (void)dtype;
+  return layout_of(a).total;
+}
+
+hipError_t oace_linear_fwd_mfma(int dtype, const OaceArgs& a, void* rows, void* ws, hipStream_t st) {
+  const Layout l = layout_of(a);
+  char* base = (char*)ws;
+  hipError_t e;
+  int64_t ldwt = 0;
+  const unsigned short* wt = wt_of(a, base, ldwt, st, e);
+  if (e != hipSuccess) return e;
+  float* part = (float*)(base + l.wt);
+  GemmArgs g = gemm_args(a, wt, ldwt);
+  g.rows = (const float*)rows;
+  g.part = part;
+  const float inv_v = (float)(1.0 / (double)a.V);
+  if ((e = launch_gemm_dt<MODE_SQ>(dtype, g, st)) != hipSuccess) return e;
+  const unsigned rg = (unsigned)((a.N + 255) / 256);
+  hipLaunchKernelGGL(oace_mfma_tau_kernel, dim3(rg), dim3(256), 0, st, (const float*)part, g.nvt, g.N, inv_v,
+                     (float)a.eps, (float*)rows);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = launch_gemm_dt<MODE_OCTIC>(dtype, g, st)) != hipSuccess) return e;
+  const unsigned wg = (unsigned)((a.N + 3) / 4);
+  if (dtype == AFA_BF16)
+    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_BF16>, dim3(wg), dim3(256), 0, st, (const float*)part, g.nvt, g.N,
+                       inv_v, (float)a.gamma, g.h, g.ldh, wt, ldwt, g.d, g.V, a.targets, (float*)rows);
+  else
+    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_F16>, dim3(wg), dim3(256), 0, st, (const float*)part, g.nvt, g.N,
+                       inv_v, (float)a.gamma, g.h, g.ldh, wt, ldwt, g.d, g.V, a.targets, (float*)rows);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return oace_mean_launch(dtype, rows, a.N, a.loss, st);
+}
+
+hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, void* ws, hipStream_t st) {
+  const Layout l = layout_of(a);
+  char* base = (char*)ws;
+  hipError_t e;
+  int64_t ldwt = 0;
+  const unsigned short* wt = wt_of(a, base, ldwt, st, e);
+  if (e != hipSuccess) return e;
+  unsigned short* dz = (unsigned short*)(base + l.wt);
+  void* bws = base + l.wt + l.dz;
+  GemmArgs g = gemm_args(a, wt, ldwt);
+  g.rows = (const float*)rows;
+  g.dz = dz;
+  g.ldz = ldz_of(a.V);
+  g.c0 = (float)(8.0 * a.gamma / (double)a.N);
+  g.g_loss = (const float*)a.g_loss;
+  if ((e = launch_gemm_dt<MODE_DZ>(dtype, g, st)) != hipSuccess) return e;
+  // dh (N, d) row-major = dz (N, V) W^T: column-major dh^T (d x N) = Wt^T-view (d x V) . dz^T-view (V x N)
+  if ((e = blas_gemm(dtype, false, false, a.d, a.N, a.V, wt, ldwt, dz, g.ldz, a.dh, a.d, bws, l.blas, st)) !=
+      hipSuccess)
+    return e;
+  if (a.w_layout == OACE_W_DV) {
+    // dW (d, V) row-major: column-major dW^T (V x d) = dz^T-view (V x N) . op_T(h-view (d x N))
+    return blas_gemm(dtype, false, true, a.V, a.d, a.N, dz, g.ldz, a.h, a.ldh, a.dw, a.ldw, bws, l.blas, st);
+  }
+  // dWt (V, d) row-major: column-major (d x V) = h-view (d x N) . op_T(dz-view (V x N))
+  return blas_gemm(dtype, false, true, a.d, a.V, a.N, a.h, a.ldh, dz, g.ldz, a.dw, a.ldw, bws, l.blas, st);
+}
+
+}  // namespace afa

@@ -39,6 +39,7 @@ enum afa_status {
   AFA_ERR_ALIGN = 9,         /* a stride or pointer breaks the required alignment */
   AFA_ERR_WORKSPACE = 10,    /* workspace too small */
   AFA_ERR_UNSUPPORTED = 11,  /* combination this build does not implement */
+  AFA_ERR_GAMMA = 12,        /* OACE gamma not finite or not positive (src/loss.py:33-34) */
   AFA_ERR_HIP = 100          /* a HIP runtime call failed; afa_last_hip_error() has the code */
 };
 
@@ -128,6 +129,52 @@ int ago_build_tables(int table_dtype, int64_t dim, int64_t max_seq_len, const vo
 int ago_rotate(int dtype, int64_t outer, int64_t seq_len, int64_t inner, int64_t dim,
                const void* x, void* y, int table_dtype, const void* rot_cos,
                const void* rot_sin, int64_t rot_len, void* stream);
+
+/*
+ * OACE loss head.  Calc type A: fp32, fp64 for AFA_F64 inputs.  targets: int64 class indices
+ * (rows of them, device memory); a target outside [0, vocab) gives an infinite loss, as in the
+ * reference.  loss: one A (device memory), the mean over rows.  row_cache: rows x
+ * OACE_ROW_FIELDS values of A per row, in this order: tau, inv_S, S^(1/8), sum p^(7/8),
+ * p_target^(-1/8), radial, loss, (unused) -- the forward writes it and the backward reads it
+ * (the cache of the reference's custom VJP).  g_loss (nullable = 1): the loss cotangent, one A
+ * in device memory.
+ *
+ * oace_linear_fwd / oace_linear_bwd replace fused_linear_oace_forward / _backward
+ * (src/kernels/pallas_oace.py:59-269) and the custom VJP fused_linear_oace (:272-293):
+ * loss = mean_n gamma (8 p_c^(-1/8) + 8/7 sum p^(7/8) - 64/7) of the A-Softmax of
+ * z = h W normalised by tau = rsqrt(mean(z^2) + eps_vocab).  h: (rows, d_model), row stride
+ * ldh.  w: OACE_W_DV, (d_model, vocab) with row stride ldw (the reference's output_head), or
+ * OACE_W_VD, (vocab, d_model) with row stride ldw (a tied token embedding, W = E^T).
+ * Backward outputs: dh (rows, d_model) contiguous, in h's dtype; dw in w's layout, dtype and
+ * ldw.  The vocabulary chunk size of the reference does not change the result and is not an
+ * argument.  workspace: oace_workspace_size() bytes of device memory, or NULL to let the call
+ * allocate and free it on `stream`.  AFA_FLAG_GENERIC forces the generic (non-MFMA) kernels.
+ */
+#define OACE_W_DV 0
+#define OACE_W_VD 1
+#define OACE_ROW_FIELDS 8
+size_t oace_workspace_size(int dtype, int64_t rows, int64_t d_model, int64_t vocab, int w_layout,
+                           unsigned flags);
+int oace_linear_fwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, const void* h,
+                    int64_t ldh, const void* w, int w_layout, int64_t ldw, const int64_t* targets,
+                    double eps_vocab, double gamma, void* loss, void* row_cache, unsigned flags,
+                    void* workspace, size_t workspace_bytes, void* stream);
+int oace_linear_bwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, const void* h,
+                    int64_t ldh, const void* w, int w_layout, int64_t ldw, const int64_t* targets,
+                    double gamma, const void* row_cache, const void* g_loss, void* dh, void* dw,
+                    unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The same loss on given logits (rows, vocab) contiguous, and its VJP dlogits (same shape and
+ * dtype).  Replaces fused_oace_softmax_loss and its custom VJP (src/model.py:180-240); the
+ * reference evaluates in the logits dtype, this evaluates in A and rounds dlogits once.
+ */
+int oace_softmax_loss_fwd(int dtype, int64_t rows, int64_t vocab, const void* logits,
+                          const int64_t* targets, double eps, double gamma, void* loss,
+                          void* row_cache, void* stream);
+int oace_softmax_loss_bwd(int dtype, int64_t rows, int64_t vocab, const void* logits,
+                          const int64_t* targets, double gamma, const void* row_cache,
+                          const void* g_loss, void* dlogits, void* stream);
 
 #ifdef __cplusplus
 }

@@ -61,7 +61,7 @@ def test_kernel_names_unique_across_sources(lib):
 def test_status_strings(lib):
     codes = [_lib.OK, _lib.ERR_NULL, _lib.ERR_DTYPE, _lib.ERR_SHAPE, _lib.ERR_HEAD_DIM, _lib.ERR_SINK,
              _lib.ERR_VALID_LEN, _lib.ERR_EPS, _lib.ERR_ROTARY, _lib.ERR_ALIGN, _lib.ERR_WORKSPACE,
-             _lib.ERR_UNSUPPORTED, _lib.ERR_HIP]
+             _lib.ERR_UNSUPPORTED, _lib.ERR_GAMMA, _lib.ERR_HIP]
     texts = [lib.afa_status_string(c).decode() for c in codes]
     assert all(texts) and len(set(texts)) == len(texts)
     assert lib.afa_status_string(12345).decode()
@@ -120,3 +120,35 @@ def test_asoftmax_octic_ago_reject_invalid_arguments(lib):
     assert lib.ago_build_tables(_lib.AFA_F32, 7, 16, None, 1e4, DUMMY, DUMMY, None) == _lib.ERR_SHAPE
     assert lib.ago_rotate(_lib.AFA_F32, 1, 16, 1, 8, DUMMY, DUMMY, _lib.AFA_F32, DUMMY, DUMMY, 15,
                           None) == _lib.ERR_ROTARY
+
+
+def test_oace_rejects_invalid_arguments(lib):
+    def fwd(dtype=_lib.AFA_BF16, N=4, d=64, V=100, h=DUMMY, ldh=64, layout=0, ldw=100, t=DUMMY, eps=100.0,
+            gamma=2.0, loss=DUMMY):
+        return lib.oace_linear_fwd(dtype, N, d, V, h, ldh, DUMMY, layout, ldw, t, eps, gamma, loss, None, 0,
+                                   None, 0, None)
+    assert fwd(dtype=5) == _lib.ERR_DTYPE
+    assert fwd(h=None) == _lib.ERR_NULL
+    assert fwd(t=None) == _lib.ERR_NULL
+    assert fwd(loss=None) == _lib.ERR_NULL
+    assert fwd(N=0) == _lib.ERR_SHAPE
+    assert fwd(V=-1) == _lib.ERR_SHAPE
+    assert fwd(layout=2) == _lib.ERR_SHAPE
+    assert fwd(ldh=63) == _lib.ERR_SHAPE
+    assert fwd(ldw=99) == _lib.ERR_SHAPE
+    assert fwd(layout=1, ldw=63) == _lib.ERR_SHAPE
+    assert fwd(eps=-1.0) == _lib.ERR_EPS
+    assert fwd(eps=math.nan) == _lib.ERR_EPS
+    assert fwd(gamma=0.0) == _lib.ERR_GAMMA
+    assert fwd(gamma=math.inf) == _lib.ERR_GAMMA
+    # an explicit workspace smaller than required is refused before any device work
+    assert lib.oace_linear_fwd(_lib.AFA_BF16, 4, 64, 100, DUMMY, 64, DUMMY, 0, 100, DUMMY, 100.0, 2.0, DUMMY,
+                               None, 0, DUMMY, 16, None) == _lib.ERR_WORKSPACE
+    assert lib.oace_linear_bwd(_lib.AFA_BF16, 4, 64, 100, DUMMY, 64, DUMMY, 0, 100, DUMMY, 2.0, None, None,
+                               DUMMY, DUMMY, 0, None, 0, None) == _lib.ERR_NULL
+    assert lib.oace_workspace_size(_lib.AFA_BF16, 512, 768, 50257, 0, 0) > 512 * 50257 * 2
+    assert lib.oace_workspace_size(_lib.AFA_BF16, 0, 768, 50257, 0, 0) == 0
+    assert lib.oace_softmax_loss_fwd(_lib.AFA_F32, 4, 9, DUMMY, DUMMY, 100.0, -2.0, DUMMY, None,
+                                     None) == _lib.ERR_GAMMA
+    assert lib.oace_softmax_loss_bwd(_lib.AFA_F32, 4, 9, DUMMY, DUMMY, 2.0, None, None, DUMMY,
+                                     None) == _lib.ERR_NULL
