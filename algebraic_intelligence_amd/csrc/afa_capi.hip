@@ -371,6 +371,7 @@ int oace_linear_fwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, con
   hipStream_t s = (hipStream_t)stream;
   afa::OaceArgs a = oace_args(rows, d_model, vocab, h, ldh, w, w_layout, ldw, targets, eps_vocab, gamma);
   a.loss = loss;
+  a.flags = flags & ~OACE_FLAG_WT_READY;
   const size_t need = oace_ws_size(dtype, a);
   void* ws = workspace;
   bool owned = false;
@@ -405,6 +406,7 @@ int oace_linear_bwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, con
   a.g_loss = g_loss;
   a.dh = dh;
   a.dw = dw;
+  a.flags = workspace != nullptr ? flags : flags & ~OACE_FLAG_WT_READY;
   const size_t need = oace_ws_size(dtype, a);
   void* ws = workspace;
   bool owned = false;

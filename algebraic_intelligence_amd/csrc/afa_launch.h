@@ -97,6 +97,7 @@ struct OaceArgs {
   const void* g_loss;  // backward: calc-type cotangent of the loss, nullable (= 1)
   void* dh;            // backward: (N, d) contiguous
   void* dw;            // backward: W's layout and ldw
+  unsigned flags;
 };
 size_t oace_generic_chunk_rows(int dtype, int64_t N, int64_t V);
 size_t oace_generic_workspace(int dtype, int64_t N, int64_t d, int64_t V, bool backward);

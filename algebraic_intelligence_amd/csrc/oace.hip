@@ -196,20 +196,21 @@ __global__ __launch_bounds__(256) void oace_convert_kernel(const A* x, int64_t r
 }
 
 // y (cols x rows, leading dimension ldy) = x^T for a rows x cols matrix x of 2-byte elements
-// (leading dimension ldx); 64 x 64 tiles through LDS.
+// (leading dimension ldx, rows of any alignment), rows a multiple of 8 and y 16-byte aligned with
+// ldy a multiple of 8.  A lane gathers 8 consecutive rows of one column (each load coalesced
+// across the wave's consecutive columns) and writes them as one 16-byte segment of y.
 __global__ __launch_bounds__(256) void oace_transpose16_kernel(const unsigned short* x, int64_t rows, int64_t cols,
                                                                int64_t ldx, unsigned short* y, int64_t ldy) {
-  __shared__ unsigned short t[64][66];
-  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = ty; i < 64; i += 4) {
-    const int64_t r = r0 + i, c = c0 + tx;
-    t[i][tx] = (r < rows && c < cols) ? x[r * ldx + c] : (unsigned short)0;
-  }
-  __syncthreads();
-  for (int i = ty; i < 64; i += 4) {
-    const int64_t c = c0 + i, r = r0 + tx;
-    if (c < cols && r < rows) y[c * ldy + r] = t[tx][i];
+  const int64_t c = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+  if (c >= cols) return;
+  for (int64_t r0 = ((int64_t)blockIdx.y * 4 + (threadIdx.x >> 6)) * 8; r0 < rows; r0 += (int64_t)gridDim.y * 32) {
+    unsigned v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = x[(r0 + j) * ldx + c];
+    u32x4_t w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = v[2 * e] | (v[2 * e + 1] << 16);
+    *(u32x4_t*)(y + c * ldy + r0) = w;
   }
 }
 
@@ -395,7 +396,8 @@ hipError_t oace_softmax_bwd_launch(int dtype, const OaceArgs& a, const void* row
 
 hipError_t oace_transpose16(const void* x, int64_t rows, int64_t cols, int64_t ldx, void* y, int64_t ldy,
                             hipStream_t st) {
-  const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  if (rows % 8 != 0 || ldy % 8 != 0 || ((uintptr_t)y & 15u) != 0) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)std::min<int64_t>((rows + 31) / 32, 8));
   hipLaunchKernelGGL(oace_transpose16_kernel, grid, dim3(256), 0, st, (const unsigned short*)x, rows, cols, ldx,
                      (unsigned short*)y, ldy);
   return hipGetLastError();

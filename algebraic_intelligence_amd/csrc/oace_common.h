@@ -42,6 +42,22 @@ __device__ __forceinline__ Oct<A> octic(A x) {
   return o;
 }
 
+// Branch-free fp32 octic parts: rho = fma(1 + x^2, rsqrt(1 + x^2), x) for both signs.  For x < 0
+// this cancels, but the absolute error of rho^7, rho^8 stays below ~1e-7 there (rho < 1), far
+// below the resolution of sums over a vocabulary of such terms, which is where it is used; the
+// target's rho is always taken from the two-branch form.
+__device__ __forceinline__ Oct<float> octic_fast(float x) {
+  const float t = __builtin_fmaf(x, x, 1.0f);
+  Oct<float> o;
+  o.r = __builtin_amdgcn_rsqf(t);
+  o.rho = __builtin_fmaf(t, o.r, x);
+  const float k2 = o.rho * o.rho;
+  const float k4 = k2 * k2;
+  o.k8 = k4 * k4;
+  o.rho7 = o.rho * k2 * k4;
+  return o;
+}
+
 // Row record from the forward sums (pallas_oace.py:166-187).
 template <typename A>
 __device__ __forceinline__ void oace_finalize_row(A* rec, A tau, A s0, A s1, A s2, A s3, A rho_t, A rn_t,

@@ -20,7 +20,9 @@
 // of one vocabulary block are dispatched consecutively on one XCD (they share its W tile in L2).
 // W is used as W^T (vocab, d_model) with d_model contiguous: a tied embedding already is; the
 // (d_model, vocab) output head is transposed once per call into the workspace.
+#include <map>
 #include <mutex>
+#include <tuple>
 #include <type_traits>
 
 #include <hipblaslt/hipblaslt.h>
@@ -184,36 +186,45 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
       const int n = n0 + nb * 32 + l32;
       tau[nb] = n < a.N ? a.rows[(int64_t)n * OACE_ROW + OACE_TAU] : 0.f;
     }
-    // masks only in the last vocabulary tile (uniform branch)
-    auto sums = [&](auto masked) {
-      const int vlim = a.V - vw - 4 * g;  // entries e with 32 vb + 8 (e >> 2) + (e & 3) < vlim exist
+    // Entries past the vocabulary (last tile only) are set to z = 0, whose octic terms are exact:
+    // rho = 1, so each adds 1 to sum k8 and sum rho7 and 0 to the r x sums; those counts are
+    // subtracted below.  One code path for every tile keeps the epilogue within the registers.
+    float nmask = 0.f;
+    if (vtail) {
+      const int vlim = a.V - vw - 4 * g;  // valid offsets 32 vb + 8 (e >> 2) + (e & 3) < vlim
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
-        for (int vb = 0; vb < 2; ++vb)
+        for (int e = 0; e < 16; ++e) {
+          const bool out = 32 * vb + 8 * (e >> 2) + (e & 3) >= vlim;
+          nmask += out ? 1.f : 0.f;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const float x = acc[vb][nb][e] * tau[nb];
-            const Oct<float> o = octic(x);
-            const float rn = o.r * x;
-            const bool in = !decltype(masked)::value || 32 * vb + 8 * (e >> 2) + (e & 3) < vlim;
-            s[0] += in ? o.k8 : 0.f;
-            s[1] += in ? o.rho7 : 0.f;
-            s[2] += in ? rn * o.k8 : 0.f;
-            s[3] += in ? rn * o.rho7 : 0.f;
-          }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float x = s[q] + __shfl_xor(s[q], 32);
-          if (g == 0) red[(wave * 4 + q) * TN + nb * 32 + l32] = x;
+          for (int nb = 0; nb < 4; ++nb) acc[vb][nb][e] = out ? 0.f : acc[vb][nb][e];
         }
-        // keep the row blocks apart: interleaving their octic chains costs more registers than exist
-        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      float s[4] = {-nmask, -nmask, 0.f, 0.f};
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float x = acc[vb][nb][e] * tau[nb];
+          const Oct<float> o = octic_fast(x);
+          const float rn = o.r * x;
+          s[0] += o.k8;
+          s[1] += o.rho7;
+          s[2] += rn * o.k8;
+          s[3] += rn * o.rho7;
+          // bound the octic chains in flight (each holds x and r): 8 at a time fit the registers
+          if ((e & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float x = s[q] + __shfl_xor(s[q], 32);
+        if (g == 0) red[(wave * 4 + q) * TN + nb * 32 + l32] = x;
       }
-    };
-    if (vtail) sums(std::true_type{});
-    else sums(std::false_type{});
+    }
     __syncthreads();
     for (int i = tid; i < TN * 4; i += 256) {
       const int q = i / TN, nl = i % TN;
@@ -243,7 +254,7 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const float x = acc[vb][nb][4 * e4 + u] * tau;
-            const Oct<float> o = octic(x);
+            const Oct<float> o = octic_fast(x);  // error far below the rounding of dz to the element type
             const float bracket = scale * o.rho7 - (vs + u == t ? pc : 0.f) - (o.k8 * inv_S) * diff;
             dzv[u] = tc * (o.r * bracket - radial * x);
           }
@@ -261,11 +272,14 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
 // tau per row from the MODE_SQ partials, summed over vocabulary tiles in order.
 __global__ __launch_bounds__(256) void oace_mfma_tau_kernel(const float* part, int nvt, int N, float inv_v, float eps,
                                                             float* rows) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per row
   if (n >= N) return;
   float ss = 0.f;
-  for (int t = 0; t < nvt; ++t) ss += part[(int64_t)t * N + n];
-  rows[(int64_t)n * OACE_ROW + OACE_TAU] = o_rsq<float>(ss * inv_v + eps);
+  for (int t = lane; t < nvt; t += 64) ss += part[(int64_t)t * N + n];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+  if (lane == 0) rows[(int64_t)n * OACE_ROW + OACE_TAU] = o_rsq<float>(ss * inv_v + eps);
 }
 
 // Row records from the MODE_OCTIC partials, one wave per row.  The target logit is the dot
@@ -314,6 +328,17 @@ __global__ __launch_bounds__(256) void oace_mfma_rows_kernel(const float* part, 
   }
 }
 
+// dh = sum of the split-K partials (fixed order), rounded once to the element type.
+template <int DT>
+__global__ __launch_bounds__(256) void oace_mfma_splitk_sum_kernel(const float* part, int parts, int64_t n,
+                                                                   unsigned short* out) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float s = 0.f;
+    for (int p = 0; p < parts; ++p) s += part[p * n + i];
+    Elem<DT>::store(out, i, s);
+  }
+}
+
 // ------------------------------------------------------------------------------ host side
 namespace {
 
@@ -325,20 +350,26 @@ constexpr size_t BLAS_WS = (size_t)64 << 20;
 
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+int dh_splits(const OaceArgs& a);
+
 struct Layout {
-  size_t wt, part, dz, blas, total;
+  size_t wt, part, dz, dhp, blas, total;
 };
 Layout layout_of(const OaceArgs& a) {
   Layout l;
   l.wt = a.w_layout == OACE_W_DV ? al((size_t)a.V * a.d * 2) : 0;
   l.part = al((size_t)nvt_of(a.V) * a.N * 4 * sizeof(float));
   l.dz = al((size_t)a.N * ldz_of(a.V) * 2);
+  const int s = dh_splits(a);
+  l.dhp = s > 1 ? al((size_t)(s + 1) * a.d * a.N * sizeof(float)) : 0;  // split-K partials of dh
   l.blas = BLAS_WS;
-  l.total = l.wt + std::max(l.part, l.dz + l.blas);
+  l.total = l.wt + std::max(l.part, l.dz + l.dhp + l.blas);
   return l;
 }
 
-// W^T (V, d) with d contiguous: the caller's tied embedding, or a transposed copy in ws.
+// W^T (V, d) with d contiguous: the caller's tied embedding, or a transposed copy at the start of
+// the workspace -- made here, or left there by a forward call on the same workspace and weights
+// (OACE_FLAG_WT_READY, the caller's guarantee).
 const unsigned short* wt_of(const OaceArgs& a, void* ws, int64_t& ldwt, hipStream_t st, hipError_t& e) {
   e = hipSuccess;
   if (a.w_layout == OACE_W_VD) {
@@ -346,7 +377,7 @@ const unsigned short* wt_of(const OaceArgs& a, void* ws, int64_t& ldwt, hipStrea
     return (const unsigned short*)a.w;
   }
   ldwt = a.d;
-  e = oace_transpose16(a.w, a.d, a.V, a.ldw, ws, a.d, st);
+  if (!(a.flags & OACE_FLAG_WT_READY)) e = oace_transpose16(a.w, a.d, a.V, a.ldw, ws, a.d, st);
   return (const unsigned short*)ws;
 }
 
@@ -389,39 +420,145 @@ hipblasLtHandle_t blas_handle() {
 }
 
 // Column-major D (m x n, ldd) = op(A) op(B), k the contraction; A stored (ta ? k x m : m x k) with
-// lda, B stored (tb ? n x k : k x n) with ldb; fp32 accumulation, element-type output.
-hipError_t blas_gemm(int dtype, bool ta, bool tb, int64_t m, int64_t n, int64_t k, const void* A, int64_t lda,
-                     const void* B, int64_t ldb, void* D, int64_t ldd, void* ws, size_t wsb, hipStream_t st) {
+// lda, B stored (tb ? n x k : k x n) with ldb; fp32 accumulation; D in the element type, or fp32
+// when d_f32.  batch > 1: strided batches (element strides sa, sb, sd).
+struct BlasGemm {
+  bool ta, tb;
+  int64_t m, n, k;
+  const void* A;
+  int64_t lda, sa;
+  const void* B;
+  int64_t ldb, sb;
+  void* D;
+  int64_t ldd, sd;
+  bool d_f32;
+  int batch;
+};
+
+// The heuristic's first choice can be far from the best kernel for these shapes (a small output
+// with a long contraction, or the reverse), so the first call for a shape times the heuristic's
+// top candidates once on the real operands and keeps the fastest (per device and shape).  Under
+// stream capture no timing is possible and the first candidate is used.
+constexpr int MAX_ALGOS = 8;
+struct AlgoKey {
+  int dev, dtype;
+  bool ta, tb, d_f32;
+  int batch;
+  int64_t m, n, k, lda, ldb, ldd, sa, sb, sd;
+  bool operator<(const AlgoKey& o) const {
+    return std::tie(dev, dtype, ta, tb, d_f32, batch, m, n, k, lda, ldb, ldd, sa, sb, sd) <
+           std::tie(o.dev, o.dtype, o.ta, o.tb, o.d_f32, o.batch, o.m, o.n, o.k, o.lda, o.ldb, o.ldd, o.sa, o.sb, o.sd);
+  }
+};
+std::mutex& algo_mutex() {
+  static std::mutex m;
+  return m;
+}
+std::map<AlgoKey, hipblasLtMatmulAlgo_t>& algo_cache() {
+  static std::map<AlgoKey, hipblasLtMatmulAlgo_t> c;
+  return c;
+}
+
+int tune(hipblasLtHandle_t h, hipblasLtMatmulDesc_t desc, hipblasLtMatrixLayout_t la, hipblasLtMatrixLayout_t lb,
+         hipblasLtMatrixLayout_t ld, const BlasGemm& g, const hipblasLtMatmulHeuristicResult_t* res, int found,
+         void* ws, size_t wsb, hipStream_t st) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (found < 2 || hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return 0;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return 0;
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return 0;
+  }
+  const float alpha = 1.f, beta = 0.f;
+  int best = 0;
+  float best_ms = 3.4e38f;
+  for (int i = 0; i < found; ++i) {
+    if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > wsb) continue;
+    // one untimed run (first-use costs), then one timed run
+    if (hipblasLtMatmul(h, desc, &alpha, g.A, la, g.B, lb, &beta, g.D, ld, g.D, ld, &res[i].algo, ws, wsb, st) !=
+        HIPBLAS_STATUS_SUCCESS)
+      continue;
+    float ms = 0.f;
+    if (hipEventRecord(e0, st) != hipSuccess ||
+        hipblasLtMatmul(h, desc, &alpha, g.A, la, g.B, lb, &beta, g.D, ld, g.D, ld, &res[i].algo, ws, wsb, st) !=
+            HIPBLAS_STATUS_SUCCESS ||
+        hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+      continue;
+    if (ms < best_ms) {
+      best_ms = ms;
+      best = i;
+    }
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipGetLastError();
+  return best;
+}
+
+hipError_t blas_gemm(int dtype, const BlasGemm& g, void* ws, size_t wsb, hipStream_t st) {
   hipblasLtHandle_t h = blas_handle();
   if (h == nullptr) return hipErrorNotInitialized;
   const hipDataType t = dtype == AFA_BF16 ? HIP_R_16BF : HIP_R_16F;
+  const hipDataType td = g.d_f32 ? HIP_R_32F : t;
   hipblasLtMatmulDesc_t desc = nullptr;
   hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
   hipblasLtMatmulPreference_t pref = nullptr;
   hipError_t err = hipErrorNotSupported;
-  const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  const hipblasOperation_t opa = g.ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = g.tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
   const uint64_t wsz = wsb;
-  hipblasLtMatmulHeuristicResult_t res[1];
+  const int32_t bc = g.batch;
+  hipblasLtMatmulHeuristicResult_t res[MAX_ALGOS];
   int found = 0;
   const float alpha = 1.f, beta = 0.f;
+  auto batched = [&](hipblasLtMatrixLayout_t l, int64_t stride) {
+    return hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) ==
+               HIPBLAS_STATUS_SUCCESS &&
+           hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &stride,
+                                             sizeof(stride)) == HIPBLAS_STATUS_SUCCESS;
+  };
   if (hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) goto done;
   if (hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(int32_t)) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(int32_t)) != HIPBLAS_STATUS_SUCCESS)
     goto done;
-  if (hipblasLtMatrixLayoutCreate(&la, t, ta ? k : m, ta ? m : k, lda) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&lb, t, tb ? n : k, tb ? k : n, ldb) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&ld, t, m, n, ldd) != HIPBLAS_STATUS_SUCCESS)
+  if (hipblasLtMatrixLayoutCreate(&la, t, g.ta ? g.k : g.m, g.ta ? g.m : g.k, g.lda) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&lb, t, g.tb ? g.n : g.k, g.tb ? g.k : g.n, g.ldb) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&ld, td, g.m, g.n, g.ldd) != HIPBLAS_STATUS_SUCCESS)
     goto done;
+  if (g.batch > 1 && !(batched(la, g.sa) && batched(lb, g.sb) && batched(ld, g.sd))) goto done;
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof(wsz)) !=
           HIPBLAS_STATUS_SUCCESS)
     goto done;
-  if (hipblasLtMatmulAlgoGetHeuristic(h, desc, la, lb, ld, ld, pref, 1, res, &found) != HIPBLAS_STATUS_SUCCESS ||
-      found < 1)
-    goto done;
-  if (hipblasLtMatmul(h, desc, &alpha, A, la, B, lb, &beta, D, ld, D, ld, &res[0].algo, ws, wsb, st) ==
-      HIPBLAS_STATUS_SUCCESS)
-    err = hipSuccess;
+  {
+    const AlgoKey key = {0, dtype, g.ta, g.tb, g.d_f32, g.batch, g.m, g.n, g.k, g.lda, g.ldb, g.ldd, g.sa, g.sb, g.sd};
+    AlgoKey k2 = key;
+    (void)hipGetDevice(&k2.dev);
+    const hipblasLtMatmulAlgo_t* algo = nullptr;
+    hipblasLtMatmulAlgo_t chosen;
+    {
+      std::lock_guard<std::mutex> lock(algo_mutex());
+      auto it = algo_cache().find(k2);
+      if (it != algo_cache().end()) {
+        chosen = it->second;
+        algo = &chosen;
+      }
+    }
+    if (algo == nullptr) {
+      if (hipblasLtMatmulAlgoGetHeuristic(h, desc, la, lb, ld, ld, pref, MAX_ALGOS, res, &found) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          found < 1)
+        goto done;
+      chosen = res[tune(h, desc, la, lb, ld, g, res, found, ws, wsb, st)].algo;
+      algo = &chosen;
+      std::lock_guard<std::mutex> lock(algo_mutex());
+      algo_cache()[k2] = chosen;
+    }
+    if (hipblasLtMatmul(h, desc, &alpha, g.A, la, g.B, lb, &beta, g.D, ld, g.D, ld, algo, ws, wsb, st) ==
+        HIPBLAS_STATUS_SUCCESS)
+      err = hipSuccess;
+  }
 done:
   if (pref) hipblasLtMatmulPreferenceDestroy(pref);
   if (ld) hipblasLtMatrixLayoutDestroy(ld);
@@ -429,6 +566,14 @@ done:
   if (la) hipblasLtMatrixLayoutDestroy(la);
   if (desc) hipblasLtMatmulDescDestroy(desc);
   return err;
+}
+
+// Split of the vocabulary contraction of dh = dz W^T (output only d x N, contraction V): enough
+// slices for ~512 output tiles of 128 x 128, each slice at least 1024 entries long.
+int dh_splits(const OaceArgs& a) {
+  const int64_t tiles = ((a.d + 127) / 128) * ((a.N + 127) / 128);
+  const int64_t s = std::min<int64_t>(std::max<int64_t>(1, (512 + tiles - 1) / tiles), std::max<int64_t>(1, a.V / 1024));
+  return (int)std::min<int64_t>(s, 32);
 }
 
 }  // namespace
@@ -459,7 +604,7 @@ hipError_t oace_linear_fwd_mfma(int dtype, const OaceArgs& a, void* rows, void* 
   g.part = part;
   const float inv_v = (float)(1.0 / (double)a.V);
   if ((e = launch_gemm_dt<MODE_SQ>(dtype, g, st)) != hipSuccess) return e;
-  const unsigned rg = (unsigned)((a.N + 255) / 256);
+  const unsigned rg = (unsigned)((a.N + 3) / 4);
   hipLaunchKernelGGL(oace_mfma_tau_kernel, dim3(rg), dim3(256), 0, st, (const float*)part, g.nvt, g.N, inv_v,
                      (float)a.eps, (float*)rows);
   if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -491,16 +636,42 @@ hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, 
   g.c0 = (float)(8.0 * a.gamma / (double)a.N);
   g.g_loss = (const float*)a.g_loss;
   if ((e = launch_gemm_dt<MODE_DZ>(dtype, g, st)) != hipSuccess) return e;
-  // dh (N, d) row-major = dz (N, V) W^T: column-major dh^T (d x N) = Wt^T-view (d x V) . dz^T-view (V x N)
-  if ((e = blas_gemm(dtype, false, false, a.d, a.N, a.V, wt, ldwt, dz, g.ldz, a.dh, a.d, bws, l.blas, st)) !=
-      hipSuccess)
-    return e;
+  // dh (N, d) row-major = dz (N, V) W^T: column-major dh^T (d x N) = Wt^T-view (d x V) . dz^T-view (V x N).
+  // The contraction is the whole vocabulary and the output small, so it is split into S slices of
+  // the vocabulary (a strided batch into fp32 partials, plus the remainder) and reduced in order.
+  const int S = dh_splits(a);
+  if (S == 1) {
+    if ((e = blas_gemm(dtype, {false, false, a.d, a.N, a.V, wt, ldwt, 0, dz, g.ldz, 0, a.dh, a.d, 0, false, 1}, bws,
+                       l.blas, st)) != hipSuccess)
+      return e;
+  } else {
+    float* dhp = (float*)(base + l.wt + l.dz);
+    bws = base + l.wt + l.dz + l.dhp;
+    const int64_t vs = a.V / S, rem = a.V - vs * S, dn = a.d * a.N;
+    if ((e = blas_gemm(dtype, {false, false, a.d, a.N, vs, wt, ldwt, vs * ldwt, dz, g.ldz, vs, dhp, a.d, dn, true, S},
+                       bws, l.blas, st)) != hipSuccess)
+      return e;
+    if (rem > 0 && (e = blas_gemm(dtype, {false, false, a.d, a.N, rem, wt + S * vs * ldwt, ldwt, 0, dz + S * vs, g.ldz, 0,
+                                          dhp + S * dn, a.d, 0, true, 1}, bws, l.blas, st)) != hipSuccess)
+      return e;
+    const int parts = S + (rem > 0 ? 1 : 0);
+    const unsigned grid = (unsigned)std::min<int64_t>((dn + 255) / 256, 4096);
+    if (dtype == AFA_BF16)
+      hipLaunchKernelGGL(oace_mfma_splitk_sum_kernel<AFA_BF16>, dim3(grid), dim3(256), 0, st, (const float*)dhp, parts,
+                         dn, (unsigned short*)a.dh);
+    else
+      hipLaunchKernelGGL(oace_mfma_splitk_sum_kernel<AFA_F16>, dim3(grid), dim3(256), 0, st, (const float*)dhp, parts,
+                         dn, (unsigned short*)a.dh);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   if (a.w_layout == OACE_W_DV) {
     // dW (d, V) row-major: column-major dW^T (V x d) = dz^T-view (V x N) . op_T(h-view (d x N))
-    return blas_gemm(dtype, false, true, a.V, a.d, a.N, dz, g.ldz, a.h, a.ldh, a.dw, a.ldw, bws, l.blas, st);
+    return blas_gemm(dtype, {false, true, a.V, a.d, a.N, dz, g.ldz, 0, a.h, a.ldh, 0, a.dw, a.ldw, 0, false, 1}, bws,
+                     l.blas, st);
   }
   // dWt (V, d) row-major: column-major (d x V) = h-view (d x N) . op_T(dz-view (V x N))
-  return blas_gemm(dtype, false, true, a.d, a.V, a.N, a.h, a.ldh, dz, g.ldz, a.dw, a.ldw, bws, l.blas, st);
+  return blas_gemm(dtype, {false, true, a.d, a.V, a.N, a.h, a.ldh, 0, dz, g.ldz, 0, a.dw, a.ldw, 0, false, 1}, bws,
+                   l.blas, st);
 }
 
 }  // namespace afa

@@ -19,6 +19,7 @@ __all__ = ["fused_linear_oace", "fused_linear_oace_forward", "fused_linear_oace_
 
 OACE_W_DV, OACE_W_VD = 0, 1
 ROW_FIELDS = 8
+FLAG_WT_READY = 0x10
 
 
 def _check_scalars(chunk_size=None, gamma=None):
@@ -70,19 +71,23 @@ def fused_linear_oace_forward(h, w_vocab, targets, eps_vocab: float = 100.0, gam
     N = hf.shape[0]
     loss = torch.empty((), dtype=acc, device=dev)
     rows = torch.empty((N, ROW_FIELDS), dtype=acc, device=dev)
+    code = _lib.dtype_code(h.dtype)
+    # the backward reuses this workspace (and the transposed weights the forward leaves in it)
+    wsb = _lib.lib().oace_workspace_size(code, N, d, V, layout, flags)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        rc = _lib.lib().oace_linear_fwd(_lib.dtype_code(h.dtype), N, d, V, hf.data_ptr(), hf.stride(0),
-                                        wop.data_ptr(), layout, ldw, t.data_ptr(), float(eps_vocab), float(gamma),
-                                        loss.data_ptr(), rows.data_ptr(), flags, None, 0, _lib.stream_ptr(dev))
+        rc = _lib.lib().oace_linear_fwd(code, N, d, V, hf.data_ptr(), hf.stride(0), wop.data_ptr(), layout, ldw,
+                                        t.data_ptr(), float(eps_vocab), float(gamma), loss.data_ptr(), rows.data_ptr(),
+                                        flags, ws.data_ptr(), wsb, _lib.stream_ptr(dev))
     _lib.check(rc, "oace_linear_fwd")
-    cache = (hf, w_vocab, t, rows, float(gamma), chunk_size, tuple(h.shape), flags)
+    cache = (hf, w_vocab, t, rows, float(gamma), chunk_size, tuple(h.shape), flags, ws, w_vocab._version)
     return loss, cache
 
 
 def fused_linear_oace_backward(cache, g):
     """(dh, dw_vocab, None) from the forward cache and the loss cotangent g
     (src/kernels/pallas_oace.py:212-269)."""
-    hf, w_vocab, t, rows, gamma, _chunk, shape, flags = cache
+    hf, w_vocab, t, rows, gamma, _chunk, shape, flags, ws, w_version = cache
     dev = hf.device
     d, V = w_vocab.shape
     wop, layout, ldw = _w_operand(w_vocab)
@@ -95,11 +100,13 @@ def fused_linear_oace_backward(cache, g):
     else:
         dw_store = torch.empty((V, ldw), dtype=w_vocab.dtype, device=dev)
         dw = dw_store[:, :d].t()
+    # the forward's transposed weights are still valid unless w_vocab was modified in place since
+    bflags = flags | (FLAG_WT_READY if w_vocab._version == w_version else 0)
     with torch.cuda.device(dev):
         rc = _lib.lib().oace_linear_bwd(_lib.dtype_code(hf.dtype), hf.shape[0], d, V, hf.data_ptr(), hf.stride(0),
                                         wop.data_ptr(), layout, ldw, t.data_ptr(), float(gamma), rows.data_ptr(),
-                                        gt.data_ptr(), dh.data_ptr(), dw_store.data_ptr(), flags, None, 0,
-                                        _lib.stream_ptr(dev))
+                                        gt.data_ptr(), dh.data_ptr(), dw_store.data_ptr(), bflags, ws.data_ptr(),
+                                        ws.numel(), _lib.stream_ptr(dev))
     _lib.check(rc, "oace_linear_bwd")
     return dh.reshape(shape), dw, None
 

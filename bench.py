@@ -50,6 +50,18 @@ SOFTMAX_WORKLOADS = {
     "asoftmax_bwd": (96 * 2048, 2048, "bf16", True, "algebraic_softmax VJP, (196608, 2048) bf16 scores"),
 }
 
+# Fused Linear + OACE loss head: name -> (rows N, d_model, vocab, backward, description).  The
+# reference benchmarks the forward at N=512, d_model=768, vocab=50257, bf16, (d_model, vocab)
+# output head (scripts/benchmark_kernels.py:118-183, reported as tokens/s).
+OACE_WORKLOADS = {
+    "oace": (512, 768, 50257, False, "fused_linear_oace forward, reference benchmark configuration"),
+    "oace_bwd": (512, 768, 50257, True, "fused_linear_oace backward (dh, dW), reference configuration"),
+    "oace_n8k": (8192, 768, 50257, False, "fused_linear_oace forward, 8192 rows"),
+    "oace_n8k_bwd": (8192, 768, 50257, True, "fused_linear_oace backward, 8192 rows"),
+    "oace_train": (512, 768, 50257, "step", "fused_linear_oace forward + backward, reference configuration"),
+    "oace_n8k_train": (8192, 768, 50257, "step", "fused_linear_oace forward + backward, 8192 rows"),
+}
+
 
 def parse():
     ap = argparse.ArgumentParser()
@@ -58,7 +70,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
-    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + sorted(SOFTMAX_WORKLOADS))
+    ap.add_argument("--workload", default="c3",
+                    choices=sorted(WORKLOADS) + sorted(SOFTMAX_WORKLOADS) + sorted(OACE_WORKLOADS))
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB --steps times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -158,6 +171,81 @@ def softmax_bench(args, dev):
     }), flush=True)
 
 
+def oace_bench(args, dev):
+    """Fused Linear + OACE through the C ABI (bf16, (d_model, vocab) output head, workspace
+    allocated once).  Throughput in tokens/s (the reference's metric) and MFMA TFLOP/s on the
+    algorithmic work: 2 N V d for the logits plus the cheaper of a second sweep (2 N V d) and the
+    Gram route (2 d^2 V + 2 N d^2) for the second moment; the backward is 6 N V d (recomputed
+    logits, dh, dW)."""
+    import torch
+
+    from algebraic_intelligence_amd import _lib
+
+    N, d, V, backward, workload = OACE_WORKLOADS[args.workload]
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn((N, d), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    w = torch.randn((d, V), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), generator=g, device=dev, dtype=torch.int64)
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    rows = torch.empty((N, 8), dtype=torch.float32, device=dev)
+    dh = torch.empty_like(h)
+    dw = torch.empty_like(w)
+    one = torch.ones((), dtype=torch.float32, device=dev)
+    lib = _lib.lib()
+    wsb = lib.oace_workspace_size(_lib.AFA_BF16, N, d, V, 0, 0)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def fwd():
+        r = lib.oace_linear_fwd(_lib.AFA_BF16, N, d, V, h.data_ptr(), d, w.data_ptr(), 0, V, t.data_ptr(), 100.0,
+                                2.0, loss.data_ptr(), rows.data_ptr(), 0, ws.data_ptr(), wsb, stream.cuda_stream)
+        if r != 0:
+            _lib.check(r, "oace_linear_fwd")
+
+    def bwd():
+        # same workspace as the forward: its transposed weights are reused (OACE_FLAG_WT_READY)
+        r = lib.oace_linear_bwd(_lib.AFA_BF16, N, d, V, h.data_ptr(), d, w.data_ptr(), 0, V, t.data_ptr(), 2.0,
+                                rows.data_ptr(), one.data_ptr(), dh.data_ptr(), dw.data_ptr(), 0x10, ws.data_ptr(),
+                                wsb, stream.cuda_stream)
+        if r != 0:
+            _lib.check(r, "oace_linear_bwd")
+
+    def train():
+        fwd()
+        bwd()
+
+    fwd()
+    step = train if backward == "step" else bwd if backward else fwd
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    nvd = 2 * N * V * d
+    fwd_flops = nvd + min(nvd, 2 * d * d * V + 2 * N * d * d)
+    flops = {False: fwd_flops, True: 3 * nvd, "step": fwd_flops + 3 * nvd}[backward]
+    tflops = flops / (ms * 1e-3) / 1e12
+    if not torch.isfinite(loss):
+        raise RuntimeError("non-finite loss")
+    print(json.dumps({
+        "metric": f"fused Linear+OACE {dict([(False, 'forward'), (True, 'backward'), ('step', 'forward+backward')])[backward]} "
+                  f"tokens/s (1 GPU) [{args.workload}]",
+        "value": round(N / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: h, W ~ N(0,1) bf16, uniform targets, resident in HBM",
+        "config": {"workload": workload, "rows": N, "d_model": d, "vocab": V, "w_layout": "(d_model, vocab)",
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -179,6 +267,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload in SOFTMAX_WORKLOADS:
         softmax_bench(args, dev)
+        return
+    if args.workload in OACE_WORKLOADS:
+        oace_bench(args, dev)
         return
     B, H, L, D, dt_name, causal, rot_kind, backward, workload = WORKLOADS[args.workload]
     tdt = torch.bfloat16 if dt_name == "bf16" else torch.float32

@@ -153,6 +153,10 @@ int ago_rotate(int dtype, int64_t outer, int64_t seq_len, int64_t inner, int64_t
 #define OACE_W_DV 0
 #define OACE_W_VD 1
 #define OACE_ROW_FIELDS 8
+/* oace_linear_bwd: the workspace is the one an oace_linear_fwd call with the same arguments used,
+   and the weights have not changed since; the transposed copy of an OACE_W_DV weight that call
+   left in it is reused. */
+#define OACE_FLAG_WT_READY 0x10u
 size_t oace_workspace_size(int dtype, int64_t rows, int64_t d_model, int64_t vocab, int w_layout,
                            unsigned flags);
 int oace_linear_fwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, const void* h,

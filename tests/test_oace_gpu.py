@@ -180,3 +180,18 @@ def test_target_outside_vocabulary_gives_infinite_loss(dtype, flags):
     loss, cache = _fwd(h, w, t, flags=flags)
     assert torch.isinf(cache[3][1, 6]) and torch.isfinite(cache[3][[0, 2, 3], 6]).all()
     assert torch.isinf(loss)
+
+
+def test_backward_after_weights_change_in_place():
+    """The backward reuses the transposed weights the forward left in its workspace only while
+    w_vocab is unchanged; an in-place update in between must not leave a stale copy in use."""
+    h, w, t = _case(16, 64, 700, torch.bfloat16, seed=21)
+    loss, cache = _fwd(h, w, t)
+    w.mul_(0.5)
+    dh, dw = _grads(cache, 1.0)
+    # the forward's row records belong to the old weights; the backward recomputes the logits with
+    # the current ones, exactly as the oracle backward does with those records
+    hf, wf, tn = to_f64(h), to_f64(w), t.cpu().numpy()
+    rows = {k: to_f64(cache[3][:, i:i + 1]) for i, k in enumerate(O.ROW_FIELDS)}
+    rh, rw = O.fused_linear_oace_backward(hf, wf, tn, rows, g=1.0)
+    assert normwise(to_f64(dh), rh) <= 2e-2 and normwise(to_f64(dw), rw) <= 2e-2
