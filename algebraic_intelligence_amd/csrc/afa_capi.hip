@@ -167,6 +167,29 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     }
     return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
   }
+  if (dtype == AFA_F32 && afa::f32_fwd_supported((int)head_dim) &&
+      !(flags & (AFA_FLAG_GENERIC | AFA_FLAG_EXACT_REF))) {
+    // float4 rows of v and out
+    bool ok = aligned16(v) && aligned16(out);
+    for (int i : {6, 7, 8, 9, 10, 11})
+      if (st.v[i] % 4 != 0) ok = false;
+    if (ok) {
+      afa::FwdArgs a = {};
+      a.q = q; a.k = k; a.v = v; a.out = out; a.denom = (float*)denom;
+      a.rc = (const float*)rot_cos; a.rs = (const float*)rot_sin;
+      a.q_b = st.v[0]; a.q_h = st.v[1]; a.q_l = st.v[2];
+      a.k_b = st.v[3]; a.k_h = st.v[4]; a.k_l = st.v[5];
+      a.v_b = st.v[6]; a.v_h = st.v[7]; a.v_l = st.v[8];
+      a.o_b = st.v[9]; a.o_h = st.v[10]; a.o_l = st.v[11];
+      a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len;
+      a.valid_len = vlen;
+      a.causal = causal ? 1 : 0;
+      a.q_scale = (float)(1.0 / std::sqrt((double)head_dim));
+      a.omega = (float)sink_omega;
+      a.w_unscale = 1.0f;
+      return hip_status(afa::f32_fwd_launch((int)head_dim, a, s));
+    }
+  }
   if (head_dim > 256) return AFA_ERR_UNSUPPORTED;
   afa::GenArgs g = {};
   g.q = q; g.k = k; g.v = v; g.out = out; g.denom = denom;

@@ -1,0 +1,226 @@
+// fp32 ("HIGHEST") fused AFA forward on the fp32 matrix cores (v_mfma_f32_32x32x2_f32), for
+// head_dim 32, 64 and 128.  Same contract as the generic fp32 path (src/kernels/pallas_afa.py:
+// 52-151 with fp32 operands): s = (q . k) scale in fp32, w = rho(s)^8 by the cancellation-safe
+// two-branch form, out = sum_j w v_j / (sum_j w + Omega), d = sum_j w + Omega; only the order of
+// the fp32 additions differs.
+//
+// A wave owns 32 queries; a unit is 32 keys x 32 queries.
+//   S^T = K Q^T: 32x32x2 steps over head_dim.  The two k-slots of a step are split by lane group
+//   g: group g contracts head_dim entries [g D/2, (g+1) D/2), so a lane reads its K row as
+//   contiguous 16-byte LDS fragments and keeps its query's half of q in registers.
+//   O^T += V^T P^T: the S^T accumulator of lane (query c, group g) holds keys 8 (e >> 2) + 4 g +
+//   (e & 3); contracting key (j, g) at step j makes element j of that accumulator the B operand as
+//   it is, and the A operand one V element per lane (consecutive lanes, consecutive features).
+// K/V tiles of 32 keys are staged through registers into double-buffered, padded LDS rows (the
+// Cayley rotation of k is applied in that pass, as the generic kernel does), one barrier per tile.
+// Query blocks are dispatched heaviest first (block_item).
+#include "afa_common.h"
+#include "afa_launch.h"
+
+namespace afa {
+
+namespace {
+
+constexpr int KT = 32;  // keys per tile
+
+__device__ __forceinline__ f32x16_t mma_f32(float a, float b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float rot_first(float c, float s, float x0, float x1) {
+#pragma clang fp contract(off)
+  return c * x0 - s * x1;
+}
+__device__ __forceinline__ float rot_second(float c, float s, float x0, float x1) {
+#pragma clang fp contract(off)
+  return s * x0 + c * x1;
+}
+
+}  // namespace
+
+template <int D, bool ROT>
+__global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
+  constexpr int LDR = D + 4;   // padded LDS row: consecutive rows shift by 16 bytes (no conflicts)
+  constexpr int KH = D / 2;    // head_dim entries per lane group
+  constexpr int NDB = D / 32;  // 32-feature output blocks
+  constexpr int KJOBS = KT * (D / 2) / 256;  // rotation pairs per thread per tile
+  constexpr int VJOBS = KT * (D / 4) / 256;  // float4 of V per thread per tile
+  static_assert(KJOBS >= 1 && VJOBS >= 1, "head_dim too small for the tile loader");
+  __shared__ __attribute__((aligned(16))) float ks[2][KT * LDR];
+  __shared__ __attribute__((aligned(16))) float vs[2][KT * LDR];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  int bh, qblk;
+  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
+  const int b = bh / a.H, h = bh % a.H;
+  const int L = a.L, vlen = a.valid_len;
+  const int q0_wg = qblk * 128, q0_w = q0_wg + wave * 32;
+  const int qi = q0_w + l32;
+  const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 128)) : vlen;
+  const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
+  const int ntiles = (kend_wg + KT - 1) / KT;
+  const float* qp = (const float*)a.q + b * a.q_b + h * a.q_h;
+  const float* kp = (const float*)a.k + b * a.k_b + h * a.k_h;
+  const float* vp = (const float*)a.v + b * a.v_b + h * a.v_h;
+
+  // q: lane (query qi, group g) holds features [g KH, (g+1) KH), rotated in fp32 when ROT
+  float qf[KH];
+#pragma unroll
+  for (int j = 0; j < KH; j += 2) {
+    const int d0 = g * KH + j;
+    float x0 = 0.f, x1 = 0.f;
+    if (qi < L) {
+      x0 = qp[(int64_t)qi * a.q_l + d0];
+      x1 = qp[(int64_t)qi * a.q_l + d0 + 1];
+      if constexpr (ROT) {
+        const float c = a.rc[(int64_t)qi * (D / 2) + d0 / 2], s = a.rs[(int64_t)qi * (D / 2) + d0 / 2];
+        const float y0 = rot_first(c, s, x0, x1), y1 = rot_second(c, s, x0, x1);
+        x0 = y0;
+        x1 = y1;
+      }
+    }
+    qf[j] = x0;
+    qf[j + 1] = x1;
+  }
+
+  // tile staging in registers: K as rotation pairs, V as float4
+  float kx[KJOBS][2];
+  float kc[KJOBS], ksn[KJOBS];
+  f32x4_t vx[VJOBS];
+  auto load = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < KJOBS; ++i) {
+      const int e = tid + 256 * i, r = e / (D / 2), p = e % (D / 2);
+      const int key = t * KT + r;
+      kx[i][0] = kx[i][1] = 0.f;
+      kc[i] = 1.f;
+      ksn[i] = 0.f;
+      if (key < L) {
+        kx[i][0] = kp[(int64_t)key * a.k_l + 2 * p];
+        kx[i][1] = kp[(int64_t)key * a.k_l + 2 * p + 1];
+        if constexpr (ROT) {
+          kc[i] = a.rc[(int64_t)key * (D / 2) + p];
+          ksn[i] = a.rs[(int64_t)key * (D / 2) + p];
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VJOBS; ++i) {
+      const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
+      const int key = t * KT + r;
+      f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      vx[i] = key < L ? *(const f32x4_t*)(vp + (int64_t)key * a.v_l + 4 * c4) : z;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KJOBS; ++i) {
+      const int e = tid + 256 * i, r = e / (D / 2), p = e % (D / 2);
+      float y0 = kx[i][0], y1 = kx[i][1];
+      if constexpr (ROT) {
+        y0 = rot_first(kc[i], ksn[i], kx[i][0], kx[i][1]);
+        y1 = rot_second(kc[i], ksn[i], kx[i][0], kx[i][1]);
+      }
+      ks[buf][r * LDR + 2 * p] = y0;
+      ks[buf][r * LDR + 2 * p + 1] = y1;
+    }
+#pragma unroll
+    for (int i = 0; i < VJOBS; ++i) {
+      const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
+      *(f32x4_t*)&vs[buf][r * LDR + 4 * c4] = vx[i];
+    }
+  };
+
+  f32x16_t o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+  float dsum = 0.f;
+  const float scale = a.q_scale;
+
+  if (ntiles > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) load(t + 1);  // global loads in flight during this tile's MFMAs
+    const int key0 = t * KT;
+    if (key0 < kend_w && q0_w < L) {
+      const float* kt = ks[t & 1];
+      const float* vt = vs[t & 1];
+      f32x16_t st;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) st[e] = 0.f;
+#pragma unroll
+      for (int j4 = 0; j4 < KH / 4; ++j4) {
+        const f32x4_t kv = *(const f32x4_t*)(kt + l32 * LDR + g * KH + 4 * j4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) st = mma_f32(kv[u], qf[4 * j4 + u], st);
+      }
+      const bool need_mask = (a.causal && key0 + 31 > q0_w) || key0 + 31 >= vlen || q0_w + 31 >= L;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float p = rho8_exact(st[e] * scale);
+        if (need_mask) {
+          const int key = key0 + 8 * (e >> 2) + 4 * g + (e & 3);
+          const bool keep = key < vlen && qi < L && (!a.causal || key <= qi);
+          p = keep ? p : 0.f;
+        }
+        st[e] = p;
+        dsum += p;
+      }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int kr = 8 * (j >> 2) + 4 * g + (j & 3);
+          o[db] = mma_f32(vt[kr * LDR + db * 32 + l32], st[j], o[db]);
+        }
+    }
+    // the buffer of tile t+1 was last read in tile t-1, before the previous barrier
+    if (t + 1 < ntiles) store((t + 1) & 1);
+    __syncthreads();
+  }
+
+  dsum += __shfl_xor(dsum, 32);
+  if (qi < L) {
+    const float tot = dsum + a.omega;
+    float* op = (float*)a.out + b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        f32x4_t w;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u] / tot;
+        *(f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g) = w;
+      }
+    if (a.denom != nullptr && g == 0) a.denom[(int64_t)bh * L + qi] = tot;
+  }
+}
+
+bool f32_fwd_supported(int head_dim) { return head_dim == 32 || head_dim == 64 || head_dim == 128; }
+
+template <int D>
+static hipError_t f32_launch_d(const FwdArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)(a.B * a.H * a.nqb));
+  if (a.rc != nullptr)
+    hipLaunchKernelGGL((afa_fwd_f32_kernel<D, true>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((afa_fwd_f32_kernel<D, false>), grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t f32_fwd_launch(int head_dim, FwdArgs a, hipStream_t st) {
+  a.nqb = (a.L + 127) / 128;
+  if (head_dim == 32) return f32_launch_d<32>(a, st);
+  if (head_dim == 64) return f32_launch_d<64>(a, st);
+  return f32_launch_d<128>(a, st);
+}
+
+}  // namespace afa

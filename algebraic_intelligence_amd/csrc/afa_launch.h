@@ -57,6 +57,11 @@ hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
 size_t d64_krot_bytes(const FwdArgs& a);
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream);
 
+// fp32 forward on the fp32 MFMA (afa_fwd_f32.hip): head_dim 32/64/128, V and out rows 16-byte
+// aligned; q_scale carries 1/sqrt(head_dim) (applied to the fp32 dot product).
+bool f32_fwd_supported(int head_dim);
+hipError_t f32_fwd_launch(int head_dim, FwdArgs a, hipStream_t st);
+
 hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 // MFMA backward (afa_bwd_mfma.hip): bf16/fp16, head_dim 64 or 128, seq_len a multiple of 4,
 // contiguous tensors, no rotation.  e_ws holds 2 * B*H*L floats (E, then 1/d).

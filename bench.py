@@ -356,6 +356,8 @@ def main():
         line["metric"] = METRIC.replace("at L=4096 D=64", f"at L={L} D={D}") + f" [{args.workload}]"
         if backward:
             line["metric"] = line["metric"].replace("AFA fwd", "AFA bwd")
+        if dt_name != "bf16":
+            line["metric"] = line["metric"].replace("bf16 MFMA peak", f"{dt_name} MFMA peak")
     if not args.no_cpu and args.workload == "c3":
         line["cpu_baseline"] = cpu_baseline(q, k, v, rot, args.cpu_seconds)
         line["cpu_baseline"]["gpu_speedup"] = round(tflops / line["cpu_baseline"]["value"], 1)

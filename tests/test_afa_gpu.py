@@ -233,3 +233,40 @@ def test_device_lds_limit_reported():
     p = torch.cuda.get_device_properties(0)
     print("device", p.name, "sharedMemPerBlock", getattr(p, "shared_memory_per_block", None),
           "multiProcessorCount", p.multi_processor_count)
+
+
+@pytest.mark.parametrize("shape,causal,valid,rot", [
+    ((1, 2, 256, 64), True, None, False), ((2, 3, 200, 64), False, None, True),
+    ((1, 2, 1000, 64), True, 777, True), ((1, 1, 1, 64), True, None, False),
+    ((1, 2, 130, 32), True, None, True), ((2, 1, 392, 128), False, 300, False),
+    ((1, 2, 256, 128), True, None, True), ((3, 5, 129, 64), True, None, False),
+])
+def test_fp32_mfma_vs_generic_and_fp64(shape, causal, valid, rot):
+    """The fp32 matrix-core kernel (afa_fwd_f32.hip) against the generic fp32 kernel
+    (AFA_FLAG_GENERIC) and the float64 oracle: the same fp32 contract in another summation order."""
+    B, H, L, D = shape
+    q, k, v = make_qkv(shape, torch.float32, seed=sum(shape) + 3)
+    rotary = None
+    qr, kr = to_f64(q), to_f64(k)
+    if rot:
+        rotary = A.build_cayley_rotary_matrix(D, L, freqs=torch.from_numpy(_c3_freqs(D)).cuda())
+        c, s = rotary.c.double().cpu().numpy(), rotary.s.double().cpu().numpy()
+        qr, kr = O.rotate_pairs(qr, c, s), O.rotate_pairs(kr, c, s)
+    a, da = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
+    b, db = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_GENERIC)
+    ref, dref = O.afa_forward(qr, kr, to_f64(v), 0.5, causal, valid, return_denominator=True)
+    e_g, e_r = normwise(to_f64(a), to_f64(b)), normwise(to_f64(a), ref)
+    print(f"fp32 {shape} causal={causal} valid={valid} rot={rot}: vs generic {e_g:.2e} vs fp64 {e_r:.2e}")
+    assert e_g <= 1e-5 and e_r <= 1e-5
+    assert normwise(to_f64(da), dref) <= 1e-5
+
+
+def test_fp32_strided_model_layout():
+    """(B, T, H, D).transpose(1, 2) fp32 views run the matrix-core kernel with the strides."""
+    B, T, H, D = 2, 300, 4, 64
+    rng = np.random.default_rng(19)
+    base = [torch.from_numpy(rng.standard_normal((B, T, H, D))).float().cuda() for _ in range(3)]
+    views = [x.transpose(1, 2) for x in base]
+    y_view = A.pallas_afa_forward(*views, causal=True, block_q=100, block_k=100)
+    y_cont = A.pallas_afa_forward(*[x.contiguous() for x in views], causal=True, block_q=100, block_k=100)
+    assert torch.equal(y_view, y_cont)
