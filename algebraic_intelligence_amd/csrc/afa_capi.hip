@@ -165,6 +165,8 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
         return hip_status(e);
       }
     }
+    if (head_dim == 128 && rot_cos == nullptr && !(flags & AFA_FLAG_SIMPLE_SCHEDULE))
+      return hip_status(afa::d128_fwd_launch(dtype, a, exact, s));
     return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
   }
   if (dtype == AFA_F32 && afa::f32_fwd_supported((int)head_dim) &&

@@ -56,6 +56,9 @@ hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
 // rotary tables it first rotates k into `krot` (d64_krot_bytes(a) bytes of device memory).
 size_t d64_krot_bytes(const FwdArgs& a);
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream);
+// Software-pipelined head_dim-128 kernel without rotary tables (afa_fwd_d128.hip); 128 queries
+// per workgroup.
+hipError_t d128_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);
 
 // fp32 forward on the fp32 MFMA (afa_fwd_f32.hip): head_dim 32/64/128, V and out rows 16-byte
 // aligned; q_scale carries 1/sqrt(head_dim) (applied to the fp32 dot product).

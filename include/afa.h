@@ -49,8 +49,8 @@ enum afa_status {
 #define AFA_FLAG_EXACT_REF 0x4u    /* exact_afa_reference contract: q*scale rounded to the input
                                       dtype before the dot, row sum of P cast to v.dtype, and
                                       out = o * (1/(D+Omega)) (pallas_afa.py:283-297) */
-#define AFA_FLAG_SIMPLE_SCHEDULE 0x8u /* head_dim 64: use the non-pipelined MFMA kernel (the
-                                         reference point for the pipelined one) */
+#define AFA_FLAG_SIMPLE_SCHEDULE 0x8u /* bf16/fp16 head_dim 64 and 128: use the non-pipelined
+                                         MFMA kernel (the reference point for the pipelined ones) */
 
 const char* afa_status_string(int status);
 int afa_last_hip_error(void);

@@ -270,3 +270,24 @@ def test_fp32_strided_model_layout():
     y_view = A.pallas_afa_forward(*views, causal=True, block_q=100, block_k=100)
     y_cont = A.pallas_afa_forward(*[x.contiguous() for x in views], causal=True, block_q=100, block_k=100)
     assert torch.equal(y_view, y_cont)
+
+
+@pytest.mark.parametrize("shape,causal,valid", [
+    ((1, 1, 1, 128), True, None), ((1, 1, 32, 128), False, None), ((2, 3, 96, 128), True, None),
+    ((1, 2, 300, 128), True, None), ((1, 2, 300, 128), False, 257), ((3, 5, 513, 128), True, 400),
+    ((1, 1, 1024, 128), False, None), ((2, 4, 1000, 128), True, None),
+])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_pipelined_d128_edge_shapes(shape, causal, valid, dt):
+    """The software-pipelined head_dim-128 kernel (afa_fwd_d128.hip) against the simple MFMA
+    kernel and the C contract on ragged and tiny lengths, valid_len tails and odd head counts."""
+    scale = 1.0 if dt == torch.bfloat16 else 0.3
+    q, k, v = make_qkv(shape, dt, seed=sum(shape) + 1, scale=scale)
+    a, da = _fwd(q, k, v, causal=causal, valid=valid)
+    b, db = _fwd(q, k, v, causal=causal, valid=valid, flags=_lib.FLAG_SIMPLE_SCHEDULE)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid)
+    assert np.isfinite(to_f64(a)).all()
+    e_s, e_c = normwise(to_f64(a), to_f64(b)), normwise(to_f64(a), c_out)
+    print(f"d128 {shape} causal={causal} valid={valid} {dt}: vs simple {e_s:.2e} vs contract {e_c:.2e}")
+    assert e_s <= 4e-3 and e_c <= 4e-3
+    assert normwise(to_f64(da), c_den) <= 1e-5
