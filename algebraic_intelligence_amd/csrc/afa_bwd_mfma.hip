@@ -21,6 +21,7 @@
 // elements with 16-byte chunks XOR-swizzled by (row & 7) (conflict-free 32-row fragments).
 // 1/sqrt(D) is split into a power of two folded into the register-resident operand (exact) and,
 // for D = 128, a factor 1/sqrt(2) applied to the fp32 score (the same rounding as s * scale).
+#include <algorithm>
 #include <type_traits>
 
 #include "afa_common.h"
@@ -85,6 +86,22 @@ __device__ __forceinline__ u32x4_t frag_tr(const unsigned short* tile, int r0, i
   return f;
 }
 
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+
+// Rotate the gradients of features f .. f+3 (two (even, odd) pairs, accumulator elements
+// e0 .. e0+3 of one lane) back through R^T: (g0, g1) -> (c g0 + s g1, c g1 - s g0), with the
+// fp32 Cayley tables at `trow` = position * D/2 + f/2.
+__device__ __forceinline__ void unrotate4(f32x16_t& acc, int e0, const float* rc, const float* rs, int64_t trow) {
+  const f32x2_t c = *(const f32x2_t*)(rc + trow);
+  const f32x2_t s = *(const f32x2_t*)(rs + trow);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float x0 = acc[e0 + 2 * p], x1 = acc[e0 + 2 * p + 1];
+    acc[e0 + 2 * p] = c[p] * x0 + s[p] * x1;
+    acc[e0 + 2 * p + 1] = c[p] * x1 - s[p] * x0;
+  }
+}
+
 __host__ __device__ constexpr int vm_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
 // rho(s)^8 and r = rsqrt(1 + s^2).  EXACT: two-branch (rho(|s|)^8, reciprocal for s < 0);
@@ -121,6 +138,37 @@ __global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a)
   if (row < rows && sub == 0) {
     ((float*)a.e_ws)[row] = part;
     ((float*)a.e_ws)[rows + row] = 1.0f / ((const float*)a.dtot)[row];
+  }
+}
+
+// Cayley rotation of q (blockIdx.y = 0) and k (blockIdx.y = 1) into contiguous scratch: each
+// (even, odd) pair -> (c x0 - s x1, s x0 + c x1) in fp32 with the (L, D/2) fp32 tables, rounded
+// once to the element type -- the operands the forward's loaders form.  One 16-byte chunk (four
+// pairs) per thread and step.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void afa_bwd_mfma_rotate_kernel(const GenArgs a, unsigned short* qr,
+                                                                  unsigned short* kr) {
+#pragma clang fp contract(off)
+  constexpr int CH = D / 8;
+  const int64_t chunks = (int64_t)a.B * a.H * a.L * CH;
+  const unsigned short* src = (const unsigned short*)(blockIdx.y == 0 ? a.q : a.k);
+  unsigned short* dst = blockIdx.y == 0 ? qr : kr;
+  const float* rc = (const float*)a.rc;
+  const float* rs = (const float*)a.rs;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / CH;
+    const int c = (int)(i - row * CH);
+    const int64_t t = (row % a.L) * (D / 2) + c * 4;
+    const u32x4_t w = *(const u32x4_t*)(src + i * 8);
+    const f32x4_t cc = *(const f32x4_t*)(rc + t);
+    const f32x4_t ss = *(const f32x4_t*)(rs + t);
+    u32x4_t r;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float x0 = Elem<DT>::lo(w[p]), x1 = Elem<DT>::hi(w[p]);
+      r[p] = Elem<DT>::pack(cc[p] * x0 - ss[p] * x1, ss[p] * x0 + cc[p] * x1);
+    }
+    *(u32x4_t*)(dst + i * 8) = r;
   }
 }
 
@@ -250,6 +298,14 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   }
 
   if (qi < L) {
+    if (a.rc != nullptr) {  // q was rotated: dq = R^T (dL/d(Rq))
+#pragma unroll
+      for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          unrotate4(dq[fb], 4 * r4, (const float*)a.rc, (const float*)a.rs,
+                    (int64_t)qi * (D / 2) + fb * 16 + r4 * 4 + 2 * g);
+    }
     unsigned short* op = (unsigned short*)a.out + base + (int64_t)qi * D;
 #pragma unroll
     for (int fb = 0; fb < NFB; ++fb)
@@ -415,6 +471,14 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   }
 
   if (kj < L) {
+    if (a.rc != nullptr) {  // k was rotated: dk = R^T (dL/d(Rk))
+#pragma unroll
+      for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          unrotate4(dk[fb], 4 * r4, (const float*)a.rc, (const float*)a.rs,
+                    (int64_t)kj * (D / 2) + fb * 16 + r4 * 4 + 2 * g);
+    }
     unsigned short* kout = (unsigned short*)a.dk + base + (int64_t)kj * D;
     unsigned short* vout = (unsigned short*)a.dv + base + (int64_t)kj * D;
 #pragma unroll
@@ -438,9 +502,21 @@ bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len) {
          seq_len % 4 == 0;
 }
 
+size_t mfma_bwd_rot_bytes(const GenArgs& a) { return (size_t)a.B * a.H * a.L * a.D * 2 * 2; }
+
 template <int DT, int D, bool EXACT>
-static hipError_t bwd_launch(const GenArgs& a, hipStream_t st) {
+static hipError_t bwd_launch(GenArgs a, void* rot_scratch, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.H * a.L;
+  if (a.rc != nullptr) {
+    if (rot_scratch == nullptr) return hipErrorInvalidValue;
+    unsigned short* qr = (unsigned short*)rot_scratch;
+    unsigned short* kr = qr + rows * D;
+    const int64_t chunks = rows * (D / 8);
+    const unsigned gx = (unsigned)std::min<int64_t>((chunks + 255) / 256, 4096);
+    hipLaunchKernelGGL((afa_bwd_mfma_rotate_kernel<DT, D>), dim3(gx, 2), dim3(256), 0, st, a, qr, kr);
+    a.q = qr;
+    a.k = kr;
+  }
   hipLaunchKernelGGL((afa_bwd_mfma_prep_kernel<DT>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, st, a);
   const int nb = a.B * a.H * ((a.L + 127) / 128);
   hipLaunchKernelGGL((afa_bwd_mfma_dq_kernel<DT, D, EXACT>), dim3(nb), dim3(256), 0, st, a);
@@ -449,14 +525,14 @@ static hipError_t bwd_launch(const GenArgs& a, hipStream_t st) {
 }
 
 template <int DT>
-static hipError_t bwd_launch_dt(const GenArgs& a, bool exact, hipStream_t st) {
-  if (a.D == 64) return exact ? bwd_launch<DT, 64, true>(a, st) : bwd_launch<DT, 64, false>(a, st);
-  return exact ? bwd_launch<DT, 128, true>(a, st) : bwd_launch<DT, 128, false>(a, st);
+static hipError_t bwd_launch_dt(const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st) {
+  if (a.D == 64) return exact ? bwd_launch<DT, 64, true>(a, rot_scratch, st) : bwd_launch<DT, 64, false>(a, rot_scratch, st);
+  return exact ? bwd_launch<DT, 128, true>(a, rot_scratch, st) : bwd_launch<DT, 128, false>(a, rot_scratch, st);
 }
 
-hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, hipStream_t st) {
-  if (dtype == AFA_BF16) return bwd_launch_dt<AFA_BF16>(a, exact, st);
-  return bwd_launch_dt<AFA_F16>(a, exact, st);
+hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st) {
+  if (dtype == AFA_BF16) return bwd_launch_dt<AFA_BF16>(a, exact, rot_scratch, st);
+  return bwd_launch_dt<AFA_F16>(a, exact, rot_scratch, st);
 }
 
 }  // namespace afa

@@ -24,11 +24,19 @@ size_t elem_size(int dt) { return dt == AFA_F64 ? 8 : dt == AFA_F32 ? 4 : 2; }
 size_t acc_size(int dt) { return dt == AFA_F64 ? 8 : 4; }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// The branch-free rho^8 for s < 0 carries, beyond a relative error of 32 * 2^-24, an absolute
-// cancellation error below 1e-8 per weight (a float32 sweep of s in [-1e4, 0] with the
-// hardware rsqrt off by up to one ulp gives 9.3e-9).  Over n keys that adds at most
-// n * 1e-8 / sink_omega to the relative error of out, and the fast form is used only where
-// this stays below 1e-3 (the bf16 rounding of P alone is 2e-3); never for fp32/fp64 inputs.
+// Compute units of the current device (cached per device; 256 if the query fails).
+int cu_count() {
+  static std::once_flag once[64];
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::call_once(once[dev], [dev]() {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  });
+  return cus[dev];
+}
+
 // Stream-ordered scratch from the current device's default memory pool.  The pool's release
 // threshold is raised once per device so that memory freed by one call is reused by the next
 // instead of being unmapped at every synchronisation.  Returns nullptr on failure.
@@ -51,6 +59,11 @@ void* scratch_alloc(size_t bytes, hipStream_t s) {
   return p;
 }
 
+// The branch-free rho^8 for s < 0 carries, beyond a relative error of 32 * 2^-24, an absolute
+// cancellation error below 1e-8 per weight (a float32 sweep of s in [-1e4, 0] with the
+// hardware rsqrt off by up to one ulp gives 9.3e-9).  Over n keys that adds at most
+// n * 1e-8 / sink_omega to the relative error of out, and the fast form is used only where
+// this stays below 1e-3 (the bf16 rounding of P alone is 2e-3); never for fp32/fp64 inputs.
 bool fast_rho_ok(double sink_omega, int64_t seq_len) {
   return sink_omega > 0.0 && (double)seq_len * 1e-8 / sink_omega < 1e-3;
 }
@@ -153,11 +166,20 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     if (head_dim == 64 && !(flags & AFA_FLAG_SIMPLE_SCHEDULE)) {
       afa::FwdArgs b = a;
       b.nqb = (int)((seq_len + 255) / 256);
+      // 256-query workgroups at two per CU; with fewer than that many workgroups the 32-query
+      // kernel (128-query workgroups, three per CU) fills the chip better
+      const bool small = (int64_t)b.B * b.H * b.nqb < 2 * (int64_t)cu_count();
       void* krot = nullptr;
       if (rot_cos != nullptr) krot = scratch_alloc(afa::d64_krot_bytes(b), s);
       // without scratch for the rotated k, the single fused kernel below rotates at tile load
       if (rot_cos == nullptr || krot != nullptr) {
-        hipError_t e = afa::d64_fwd_launch(dtype, b, exact, krot, s);
+        hipError_t e;
+        if (small) {
+          e = krot != nullptr ? afa::d64_krot_launch(dtype, b, krot, s) : hipSuccess;
+          if (e == hipSuccess) e = afa::pipe_fwd_launch(dtype, 64, b, exact, s);
+        } else {
+          e = afa::d64_fwd_launch(dtype, b, exact, krot, s);
+        }
         if (krot != nullptr) {
           hipError_t e2 = hipFreeAsync(krot, s);
           if (e == hipSuccess) e = e2;
@@ -166,7 +188,7 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
       }
     }
     if (head_dim == 128 && rot_cos == nullptr && !(flags & AFA_FLAG_SIMPLE_SCHEDULE))
-      return hip_status(afa::d128_fwd_launch(dtype, a, exact, s));
+      return hip_status(afa::pipe_fwd_launch(dtype, 128, a, exact, s));
     return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
   }
   if (dtype == AFA_F32 && afa::f32_fwd_supported((int)head_dim) &&
@@ -256,10 +278,20 @@ int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   a.omega = sink_omega;
   const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(g) &&
                        aligned16(dq) && aligned16(dk) && aligned16(dv) && aligned16(ws) && aligned16(denom);
-  const bool use_mfma = rot_cos == nullptr && !(flags & AFA_FLAG_GENERIC) && aligned &&
-                        afa::mfma_bwd_supported(dtype, (int)head_dim, seq_len);
+  bool use_mfma = !(flags & AFA_FLAG_GENERIC) && aligned && afa::mfma_bwd_supported(dtype, (int)head_dim, seq_len) &&
+                  (rot_cos == nullptr || (aligned16(rot_cos) && aligned16(rot_sin)));
+  // rotary tables: q and k are rotated once into stream-ordered scratch (else the generic kernel)
+  void* rot = nullptr;
+  if (use_mfma && rot_cos != nullptr) {
+    rot = scratch_alloc(afa::mfma_bwd_rot_bytes(a), s);
+    if (rot == nullptr) use_mfma = false;
+  }
   const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, a.valid_len);
-  hipError_t e = use_mfma ? afa::mfma_bwd_launch(dtype, a, exact, s) : afa::generic_bwd_launch(dtype, a, s);
+  hipError_t e = use_mfma ? afa::mfma_bwd_launch(dtype, a, exact, rot, s) : afa::generic_bwd_launch(dtype, a, s);
+  if (rot != nullptr) {
+    hipError_t e2 = hipFreeAsync(rot, s);
+    if (e == hipSuccess) e = e2;
+  }
   if (owned) {
     hipError_t e2 = hipFreeAsync(ws, s);
     if (e == hipSuccess) e = e2;

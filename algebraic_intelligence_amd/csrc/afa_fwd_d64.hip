@@ -372,23 +372,29 @@ static hipError_t launch_d64(const FwdArgs& a, hipStream_t stream) {
 
 size_t d64_krot_bytes(const FwdArgs& a) { return (size_t)a.B * a.H * a.L * 64 * 2; }
 
+hipError_t d64_krot_launch(int dtype, FwdArgs& a, void* krot, hipStream_t stream) {
+  if (krot == nullptr) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((a.L + 63) / 64), (unsigned)(a.B * a.H));
+  if (dtype == AFA_BF16)
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+  else
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_F16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  a.k = krot;
+  a.k_l = 64;
+  a.k_h = (int64_t)a.L * 64;
+  a.k_b = (int64_t)a.H * a.L * 64;
+  return hipSuccess;
+}
+
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream) {
   a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
   a.w_unscale = 1.0f;
   const bool rot = a.rc != nullptr;
   if (rot) {
-    if (krot == nullptr) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.L + 63) / 64), (unsigned)(a.B * a.H));
-    if (dtype == AFA_BF16)
-      hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
-    else
-      hipLaunchKernelGGL((afa_krot_kernel<AFA_F16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
-    hipError_t e = hipGetLastError();
+    hipError_t e = d64_krot_launch(dtype, a, krot, stream);
     if (e != hipSuccess) return e;
-    a.k = krot;
-    a.k_l = 64;
-    a.k_h = (int64_t)a.L * 64;
-    a.k_b = (int64_t)a.H * a.L * 64;
   }
   if (dtype == AFA_BF16) {
     if (exact) return rot ? launch_d64<AFA_BF16, true, true>(a, stream) : launch_d64<AFA_BF16, true, false>(a, stream);

@@ -1,20 +1,25 @@
-// Fused AFA forward for head_dim 128 (bf16 / fp16 operands, fp32 accumulate) without rotary
-// tables (C5).  Same contract as afa_fwd_mfma.hip (src/kernels/pallas_afa.py:52-151).  At
-// head_dim 128 a score costs 512 MFMA FLOPs against the same ~7.5 VALU slots of the rho^8 chain
-// as at 64, so the matrix and vector work are about even and must overlap:
+// Fused AFA forward with 32 queries per wave and several waves per SIMD, for head_dim 64 and 128
+// (bf16 / fp16 operands, fp32 accumulate).  Same contract as afa_fwd_mfma.hip
+// (src/kernels/pallas_afa.py:52-151).  A score costs 4 D MFMA FLOPs against ~7.5 VALU slots of the
+// rho^8 chain, row sum and pack; one wave's MFMAs and VALU work barely overlap, so the kernel is
+// shaped for overlap ACROSS waves: while one wave runs its rho^8 chain the other waves of its
+// SIMD keep the matrix pipe busy.
 //
-//   * two waves per SIMD (at most 256 registers per wave): while one wave runs its rho^8 chain on
-//     the VALU the other's MFMAs run.  A wave owns 32 queries; unit u (32 keys) first issues
-//     S(u+1) = K Q^T (8 x 32x32x16), then rho^8 of S(u), then O += V^T P(u) (8 x 32x32x16); the K
-//     and V fragments live only around their own MFMAs, S in two register sets used alternately;
-//   * K and V reach LDS by direct global -> LDS loads in tiles of 32 keys (256-byte rows of
-//     16-byte chunks): K chunk c of row r at c ^ (r & 7) (conflict-free 32-row fragments), V
-//     chunk c at c ^ ((r & 3) << 1) (conflict-free ds_read_tr16_b64 of 4-key column slices,
-//     which give the PV MFMA's A operand in the key order of the S^T accumulator);
+//   * a wave owns 32 queries; unit u (32 keys) first issues S(u+1) = K Q^T (D/16 x 32x32x16),
+//     then rho^8 of S(u), then O += V^T P(u) (D/16 x 32x32x16).  The K and V fragments live only
+//     around their own MFMAs and S alternates between two register sets, which keeps a wave at
+//     <= 256 VGPRs (D = 128: two waves per SIMD) or <= 168 (D = 64: three waves per SIMD);
+//   * K and V reach LDS by direct global -> LDS loads in tiles of 32 keys (rows of D/8 16-byte
+//     chunks): K chunk c of row r at c ^ (r & 7) (conflict-free 32-row fragments); V chunk c at
+//     c ^ ((r & 3) << 1) for D = 128 and c ^ (((r >> 1) & 1) << 2) for D = 64 (conflict-free
+//     ds_read_tr16_b64 of 4-key column slices, which give the PV MFMA's A operand in the key
+//     order of the S^T accumulator);
 //   * LDS is a ring of NB tiles: iteration u issues tile u + NB - 1 into the buffer of tile u - 1
 //     and waits only for its own loads of tile u + 1; one barrier per tile;
-//   * 1/sqrt(128) = 2^-4 sqrt(2): 2^-4 is folded into q exactly, and sqrt(2) is either evaluated
-//     inside (rho/sqrt 2)^8 = rho^8/16 (bf16 fast path: weights and sink carry 1/16) or formed
+//   * q is scaled by 1/sqrt(D) (and Cayley-rotated in fp32 when rotary tables are given) as it is
+//     loaded; k arrives rotated (afa_krot_kernel, once per call).  At D = 128, 1/sqrt(128) =
+//     2^-4 sqrt(2): 2^-4 is folded into q exactly, and sqrt(2) is either evaluated inside
+//     (rho/sqrt 2)^8 = rho^8/16 (bf16 fast path: weights and sink carry 1/16) or formed
 //     explicitly (two-branch path, fp16);
 //   * masks only on units that cross the causal diagonal or valid_len; workgroups heaviest first.
 #include <type_traits>
@@ -30,7 +35,7 @@ typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 template <int DT>
-__device__ __forceinline__ f32x16_t mma128(u32x4_t a, u32x4_t b, f32x16_t c) {
+__device__ __forceinline__ f32x16_t mma16(u32x4_t a, u32x4_t b, f32x16_t c) {
   if constexpr (DT == AFA_BF16) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -40,11 +45,27 @@ __device__ __forceinline__ f32x16_t mma128(u32x4_t a, u32x4_t b, f32x16_t c) {
   }
 }
 
-template <int DT>
-__device__ __forceinline__ u32x4_t scale8(u32x4_t w, float scale) {
+// 8 consecutive q features (one 16-byte chunk), scaled, and Cayley-rotated in fp32 first when
+// ROT: pairs (x0, x1) -> (c x0 - s x1, s x0 + c x1), one rounding to the element type.
+template <int DT, bool ROT>
+__device__ __forceinline__ u32x4_t q_chunk(u32x4_t w, const float* cc, const float* ss, float scale) {
+#pragma clang fp contract(off)
   u32x4_t r;
+  f32x4_t c = {1.f, 1.f, 1.f, 1.f}, s = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (ROT) {
+    c = *(const f32x4_t*)cc;
+    s = *(const f32x4_t*)ss;
+  }
 #pragma unroll
-  for (int p = 0; p < 4; ++p) r[p] = Elem<DT>::pack(Elem<DT>::lo(w[p]) * scale, Elem<DT>::hi(w[p]) * scale);
+  for (int p = 0; p < 4; ++p) {
+    const float x0 = Elem<DT>::lo(w[p]), x1 = Elem<DT>::hi(w[p]);
+    float y0 = x0, y1 = x1;
+    if constexpr (ROT) {
+      y0 = c[p] * x0 - s[p] * x1;
+      y1 = s[p] * x0 + c[p] * x1;
+    }
+    r[p] = Elem<DT>::pack(y0 * scale, y1 * scale);
+  }
   return r;
 }
 
@@ -59,19 +80,40 @@ __device__ __forceinline__ float tree16x(const float (&p)[16]) {
   return a[0] + a[2];
 }
 
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9: vmcnt [3:0] and [15:14]; expcnt and
+// lgkmcnt at their no-wait maxima).
 __host__ __device__ constexpr int vm_wait(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+template <int D>
+__device__ __forceinline__ int v_swizzle(int r, int c) {
+  if constexpr (D == 128) return c ^ ((r & 3) << 1);
+  else return c ^ (((r >> 1) & 1) << 2);
+}
+
+template <int D>
+struct PipeShape {
+  static constexpr int NB = 4;                  // ring of tile buffers
+  static constexpr int WAVES_PER_EU = D == 128 ? 2 : 3;
+};
 
 }  // namespace
 
-// SM: 1 = s = sqrt(2) x evaluated as (rho/sqrt 2)^8 = rho^8/16 (weights and sink carry 1/16);
+// SM: 0 = s as formed (q carries 1/sqrt(D) exactly, D = 64);
+//     1 = s = sqrt(2) x evaluated as (rho/sqrt 2)^8 = rho^8/16 (weights and sink carry 1/16);
 //     2 = s = sqrt(2) x formed explicitly.
-template <int DT, bool EXACT, int SM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void afa_fwd_d128_kernel(const FwdArgs a) {
-  constexpr int D = 128;
+template <int D, int DT, bool EXACT, int SM, bool ROT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PipeShape<D>::WAVES_PER_EU,
+                                                                     PipeShape<D>::WAVES_PER_EU)))
+void afa_fwd_pipe_kernel(const FwdArgs a) {
   constexpr int KT = 32;                 // keys per tile = one unit
-  constexpr int NB = 4;                  // ring of tile buffers
-  constexpr int LOADS = 4;               // direct loads per thread per tile (2 K + 2 V)
+  constexpr int NB = PipeShape<D>::NB;
+  constexpr int CH = D / 8;              // 16-byte chunks per row
+  constexpr int LPT = KT * CH / 256;     // direct loads per thread per tile, each of K and V
+  constexpr int LOADS = 2 * LPT;
+  constexpr int NK = D / 16;             // 16-feature MFMA steps of S
+  constexpr int NDB = D / 32;            // 32-feature output blocks
+  static_assert(LPT >= 1 && KT * CH % 256 == 0, "tile loader shape");
+  static_assert(NB == 4, "the waits below assume at most one tile in flight beyond the next");
   __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * D];
   __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * D];
 
@@ -95,40 +137,45 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
 
   // q fragments (B operand of S^T = K Q^T): query q0_w + l32, features kc*16 + 8g .. +7
   const int qi = q0_w + l32;
-  u32x4_t qf[8];
+  u32x4_t qf[NK];
 #pragma unroll
-  for (int kc = 0; kc < 8; ++kc) {
+  for (int kc = 0; kc < NK; ++kc) {
     u32x4_t w = {0u, 0u, 0u, 0u};
-    if (qi < L) w = scale8<DT>(*(const u32x4_t*)(qp + (int64_t)qi * a.q_l + kc * 16 + 8 * g), a.q_scale);
+    if (qi < L) {
+      const int d0 = kc * 16 + 8 * g;
+      const float* cc = ROT ? a.rc + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
+      const float* ss = ROT ? a.rs + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
+      w = q_chunk<DT, ROT>(*(const u32x4_t*)(qp + (int64_t)qi * a.q_l + d0), cc, ss, a.q_scale);
+    }
     qf[kc] = w;
   }
 
-  // direct loads: slot s = tid + 256 i covers row s >> 4, physical chunk s & 15
+  // direct loads: slot s = tid + 256 i covers row s / CH, physical chunk s % CH
   auto issue_tile = [&](int t) {
     unsigned short* kd = &lds_k[t % NB][0];
     unsigned short* vd = &lds_v[t % NB][0];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int s = tid + 256 * i, r = s >> 4, pc = s & 15;
+    for (int i = 0; i < LPT; ++i) {
+      const int s = tid + 256 * i, r = s / CH, pc = s % CH;
       const int key = min(t * KT + r, L - 1);  // rows past L: finite data, masked
-      const int lk = pc ^ (r & 7), lv = pc ^ ((r & 3) << 1);
+      const int lk = pc ^ (r & 7), lv = v_swizzle<D>(r, pc);
       __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + lk * 8),
                                        (void*)(kd + (256 * i + wave * 64) * 8), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lv * 8),
                                        (void*)(vd + (256 * i + wave * 64) * 8), 16, 0, 0);
     }
   };
-  u32x4_t kf[8];
-  u32x4_t vf[4][2];
+  u32x4_t kf[NK];
+  u32x4_t vf[NDB][2];
   auto read_kf = [&](int u) {
     const unsigned short* base = &lds_k[u % NB][l32 * D];
 #pragma unroll
-    for (int kc = 0; kc < 8; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & 7)) * 8));
+    for (int kc = 0; kc < NK; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & 7)) * 8));
   };
   auto read_vf = [&](int u) {
     const unsigned short* tile = lds_v[u % NB];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         u32x4_t f;
@@ -136,8 +183,7 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
         for (int hh = 0; hh < 2; ++hh) {
           const int row = kk * 16 + hh * 8 + 4 * g + (l16 >> 2);
           const int col = db * 32 + m16 * 16 + 4 * (l16 & 3);
-          const int pc = (col >> 3) ^ ((row & 3) << 1);
-          const unsigned short* p = tile + row * D + pc * 8 + (col & 7);
+          const unsigned short* p = tile + row * D + v_swizzle<D>(row, col >> 3) * 8 + (col & 7);
           const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
           const u32x2_t w = __builtin_bit_cast(u32x2_t, v);
           f[2 * hh] = w[0];
@@ -147,9 +193,9 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
       }
   };
 
-  f32x16_t o[4];
+  f32x16_t o[NDB];
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
   float rowsum = 0.f;
@@ -166,12 +212,10 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) sA[e] = 0.f;
 #pragma unroll
-    for (int kc = 0; kc < 8; ++kc) sA = mma128<DT>(kf[kc], qf[kc], sA);
+    for (int kc = 0; kc < NK; ++kc) sA = mma16<DT>(kf[kc], qf[kc], sA);
   }
 
-  // unit u: S(u+1) = K(u+1) Q^T on the MFMA pipe first, then P(u) = rho^8(S(u)) on the VALU, then
-  // O += V(u)^T P(u).  The K and V fragments live only around their own MFMAs (two waves per
-  // SIMD fit in the registers: one wave's VALU runs while the other's MFMAs do).
+  // unit u: S(u+1) on the MFMA pipe first, then P(u) = rho^8(S(u)) on the VALU, then O += V(u)^T P(u)
   auto unit = [&](int u, f32x16_t& scur, f32x16_t& snxt) {
     if (u >= U) return;
     if (u + 1 < U) {
@@ -179,7 +223,7 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) snxt[e] = 0.f;
 #pragma unroll
-      for (int kc = 0; kc < 8; ++kc) snxt = mma128<DT>(kf[kc], qf[kc], snxt);
+      for (int kc = 0; kc < NK; ++kc) snxt = mma16<DT>(kf[kc], qf[kc], snxt);
     }
     __builtin_amdgcn_sched_barrier(0);
     float p[16];
@@ -210,13 +254,13 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] = mma128<DT>(vf[db][kk], pk[kk], o[db]);
+      for (int db = 0; db < NDB; ++db) o[db] = mma16<DT>(vf[db][kk], pk[kk], o[db]);
   };
 
   for (int u = 0; u < ntiles; ++u) {
-    // own loads of tile u+1 done (those of tile u+2 may remain), then publish them; the barrier
-    // also ends every wave's unit u-1, the last reader of the buffer reused below
-    if (u + 2 < ntiles) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS));
+    // own loads of tile u+1 done (those of later tiles may remain), then publish them; the
+    // barrier also ends every wave's unit u-1, the last reader of the buffer reused below
+    if (u + 2 < ntiles) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * (NB - 3)));
     else __builtin_amdgcn_s_waitcnt(vm_wait(0));
     __syncthreads();
     if (u + NB - 1 < ntiles) issue_tile(u + NB - 1);
@@ -230,7 +274,7 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
     unsigned short* op = (unsigned short*)a.out + b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
     const float inv = 1.0f / tot;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         u32x2_t w;
@@ -242,23 +286,36 @@ void afa_fwd_d128_kernel(const FwdArgs a) {
   }
 }
 
-template <int DT, bool EXACT, int SM>
-static hipError_t launch_d128(const FwdArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((afa_fwd_d128_kernel<DT, EXACT, SM>), dim3(a.B * a.H * a.nqb), dim3(256), 0, st, a);
+namespace {
+
+template <int D, int DT, bool EXACT, int SM>
+hipError_t launch_pipe(const FwdArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)(a.B * a.H * a.nqb));
+  if (a.rc != nullptr)
+    hipLaunchKernelGGL((afa_fwd_pipe_kernel<D, DT, EXACT, SM, true>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((afa_fwd_pipe_kernel<D, DT, EXACT, SM, false>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
-hipError_t d128_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t st) {
+}  // namespace
+
+hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t st) {
   a.nqb = (a.L + 127) / 128;
-  a.q_scale = 0.0625f;  // 2^-4 of 1/sqrt(128), exact
   a.w_unscale = 1.0f;
+  if (head_dim == 64) {
+    a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
+    if (dtype == AFA_BF16) return exact ? launch_pipe<64, AFA_BF16, true, 0>(a, st) : launch_pipe<64, AFA_BF16, false, 0>(a, st);
+    return exact ? launch_pipe<64, AFA_F16, true, 0>(a, st) : launch_pipe<64, AFA_F16, false, 0>(a, st);
+  }
+  a.q_scale = 0.0625f;  // 2^-4 of 1/sqrt(128), exact
   if (dtype == AFA_BF16) {
-    if (exact) return launch_d128<AFA_BF16, true, 2>(a, st);
+    if (exact) return launch_pipe<128, AFA_BF16, true, 2>(a, st);
     a.omega *= 0.0625f;
     a.w_unscale = 16.0f;
-    return launch_d128<AFA_BF16, false, 1>(a, st);
+    return launch_pipe<128, AFA_BF16, false, 1>(a, st);
   }
-  return exact ? launch_d128<AFA_F16, true, 2>(a, st) : launch_d128<AFA_F16, false, 2>(a, st);
+  return exact ? launch_pipe<128, AFA_F16, true, 2>(a, st) : launch_pipe<128, AFA_F16, false, 2>(a, st);
 }
 
 }  // namespace afa

@@ -56,9 +56,11 @@ hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
 // rotary tables it first rotates k into `krot` (d64_krot_bytes(a) bytes of device memory).
 size_t d64_krot_bytes(const FwdArgs& a);
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream);
-// Software-pipelined head_dim-128 kernel without rotary tables (afa_fwd_d128.hip); 128 queries
-// per workgroup.
-hipError_t d128_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);
+// Rotates k once into `krot` (d64_krot_bytes(a) bytes) and points a's k at it (head_dim 64).
+hipError_t d64_krot_launch(int dtype, FwdArgs& a, void* krot, hipStream_t stream);
+// 32 queries per wave, several waves per SIMD (afa_fwd_pipe.hip): head_dim 64 or 128, 128
+// queries per workgroup; q is rotated at load when a.rc is set, k must arrive rotated.
+hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
 
 // fp32 forward on the fp32 MFMA (afa_fwd_f32.hip): head_dim 32/64/128, V and out rows 16-byte
 // aligned; q_scale carries 1/sqrt(head_dim) (applied to the fp32 dot product).
@@ -67,9 +69,12 @@ hipError_t f32_fwd_launch(int head_dim, FwdArgs a, hipStream_t st);
 
 hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 // MFMA backward (afa_bwd_mfma.hip): bf16/fp16, head_dim 64 or 128, seq_len a multiple of 4,
-// contiguous tensors, no rotation.  e_ws holds 2 * B*H*L floats (E, then 1/d).
+// contiguous tensors.  e_ws holds 2 * B*H*L floats (E, then 1/d).  With rotary tables (fp32,
+// 16-byte aligned) q and k are first rotated into rot_scratch (mfma_bwd_rot_bytes(a) bytes) and
+// dq, dk are rotated back in the store epilogues.
 bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len);
-hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, hipStream_t st);
+size_t mfma_bwd_rot_bytes(const GenArgs& a);
+hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st);
 hipError_t generic_bwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 
 hipError_t ago_tables_launch(int table_dtype, int pairs, int len, const void* freqs, double base,

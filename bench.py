@@ -43,6 +43,8 @@ WORKLOADS = {
     "c5": (2, 16, 8192, 128, "bf16", True, None, False, "C5: AFA forward, causal, head_dim 128"),
     "c5bwd": (2, 16, 8192, 128, "bf16", True, None, True,
               "C5: AFA analytical backward (dq, dk, dv), causal, head_dim 128"),
+    "c3bwd": (8, 12, 4096, 64, "bf16", True, "c3", True,
+              "C3: AFA analytical backward (dq, dk, dv), causal, Cayley rotary"),
 }
 # A-Softmax over the last axis of (rows, cols) scores: name -> (rows, cols, dtype, backward, description)
 SOFTMAX_WORKLOADS = {
@@ -307,7 +309,8 @@ def main():
         def step():
             r = lib.afa_bwd(code, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                             den.data_ptr(), gout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                            None, None, 0, 0.5, int(causal), 0, 0, ws.data_ptr(), ws_bytes,
+                            ptr(rc), ptr(rs), L if rot is not None else 0, 0.5, int(causal), 0, 0,
+                            ws.data_ptr(), ws_bytes,
                             stream.cuda_stream)
             if r != 0:
                 _lib.check(r, "afa_bwd")

@@ -208,24 +208,43 @@ def test_generic_head_dims(D):
     assert normwise(to_f64(y), ref) <= 1e-5
 
 
-@pytest.mark.parametrize("shape,causal,valid", [
-    ((1, 1, 1, 64), True, None), ((1, 1, 32, 64), False, None), ((2, 3, 96, 64), True, None),
-    ((1, 2, 300, 64), True, None), ((1, 2, 300, 64), False, 257), ((3, 5, 513, 64), True, 400),
-    ((1, 1, 1024, 64), False, None), ((2, 4, 1000, 64), True, None),
+def _cu_count():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+@pytest.mark.parametrize("shape,causal,valid,rot", [
+    ((1, 1, 1, 64), True, None, False), ((1, 1, 32, 64), False, None, False), ((2, 3, 96, 64), True, None, True),
+    ((1, 2, 300, 64), True, None, False), ((1, 2, 300, 64), False, 257, True), ((3, 5, 513, 64), True, 400, False),
+    ((1, 1, 1024, 64), False, None, False), ((2, 4, 1000, 64), True, None, True),
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-def test_pipelined_d64_edge_shapes(shape, causal, valid, dt):
-    """The software-pipelined head_dim-64 kernel against the simple MFMA kernel and the C
-    contract on lengths that are not tile multiples, tiny lengths, valid_len tails and odd
-    batch x head counts (so the workgroup remap sees counts not divisible by 8)."""
+@pytest.mark.parametrize("wide", [False, True])
+def test_pipelined_d64_edge_shapes(shape, causal, valid, rot, dt, wide):
+    """The head_dim-64 kernels against the simple MFMA kernel and the C contract on lengths that
+    are not tile multiples, tiny lengths, valid_len tails and odd batch x head counts (so the
+    workgroup remap sees counts not divisible by 8).  Small grids take the 32-query kernel
+    (afa_fwd_pipe.hip); `wide` repeats the heads until the 256-query workgroups number at least
+    two per CU, which takes afa_fwd_d64.hip, and checks every copy of a head is bitwise equal."""
+    B, H, L, D = shape
     scale = 1.0 if dt == torch.bfloat16 else 0.4
     q, k, v = make_qkv(shape, dt, seed=sum(shape), scale=scale)
-    a, da = _fwd(q, k, v, causal=causal, valid=valid)
-    b, db = _fwd(q, k, v, causal=causal, valid=valid, flags=_lib.FLAG_SIMPLE_SCHEDULE)
-    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid)
+    rotary = A.build_cayley_rotary_matrix(D, L, freqs=_c3_freqs(D)) if rot else None
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid, rotary=rotary)
+    reps = 1
+    if wide:
+        reps = -(-2 * _cu_count() // (B * H * -(-L // 256)))
+        q, k, v = (x.repeat(1, reps, 1, 1).contiguous() for x in (q, k, v))
+    a, da = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
+    b, db = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_SIMPLE_SCHEDULE)
     assert np.isfinite(to_f64(a)).all()
     assert normwise(to_f64(a), to_f64(b)) <= 4e-3
-    assert normwise(to_f64(a), c_out) <= 4e-3
+    if wide:
+        assert torch.equal(a, a[:, :H].repeat(1, reps, 1, 1))
+        assert torch.equal(da, da[:, :H].repeat(1, reps, 1, 1))
+        a, da = a[:, :H], da[:, :H]
+    e_c = normwise(to_f64(a), c_out)
+    print(f"d64 {shape} causal={causal} valid={valid} rot={rot} {dt} wide={wide} (x{reps}): vs contract {e_c:.2e}")
+    assert e_c <= 4e-3
     assert normwise(to_f64(da), c_den) <= 1e-5
 
 
@@ -279,8 +298,8 @@ def test_fp32_strided_model_layout():
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_pipelined_d128_edge_shapes(shape, causal, valid, dt):
-    """The software-pipelined head_dim-128 kernel (afa_fwd_d128.hip) against the simple MFMA
-    kernel and the C contract on ragged and tiny lengths, valid_len tails and odd head counts."""
+    """The head_dim-128 kernel (afa_fwd_pipe.hip) against the simple MFMA kernel and the C
+    contract on ragged and tiny lengths, valid_len tails and odd head counts."""
     scale = 1.0 if dt == torch.bfloat16 else 0.3
     q, k, v = make_qkv(shape, dt, seed=sum(shape) + 1, scale=scale)
     a, da = _fwd(q, k, v, causal=causal, valid=valid)

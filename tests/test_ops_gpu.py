@@ -105,17 +105,19 @@ def test_backward_low_precision(dtype):
         assert e_r <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
 
 
-def _bwd_flags(q, k, v, out, den, g, causal, valid, flags):
-    """afa_bwd through the C ABI with explicit flags (contiguous inputs)."""
+def _bwd_flags(q, k, v, out, den, g, causal, valid, flags, rot=None):
+    """afa_bwd through the C ABI with explicit flags (contiguous inputs; rot = fp32 (cos, sin)
+    device tables or None)."""
     from algebraic_intelligence_amd import _lib
     B, H, L, D = q.shape
     dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
     code = _lib.dtype_code(q.dtype)
     ws_bytes = _lib.lib().afa_bwd_workspace_size(code, B, H, L, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    rc_p, rs_p, rlen = (None, None, 0) if rot is None else (rot[0].data_ptr(), rot[1].data_ptr(), rot[0].shape[0])
     rc = _lib.lib().afa_bwd(code, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                             den.data_ptr(), g.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                            None, None, 0, 0.5, int(causal), 0 if valid is None else valid, flags,
+                            rc_p, rs_p, rlen, 0.5, int(causal), 0 if valid is None else valid, flags,
                             ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "afa_bwd")
     return dq, dk, dv
@@ -149,6 +151,39 @@ def test_mfma_backward_vs_generic_and_contract(shape, causal, valid, dt):
         print(f"{shape} causal={causal} valid={valid} {dt} {name}: vs generic {e_g:.2e} "
               f"vs contract {e_c:.2e} vs fp64 {e_r:.2e}")
         assert e_g <= 1e-2 and e_c <= 1e-2
+        assert e_r <= 3e-2
+
+
+@pytest.mark.parametrize("shape,causal,valid", [
+    ((1, 2, 256, 64), True, None), ((2, 3, 200, 64), False, None), ((1, 2, 1000, 64), True, 777),
+    ((1, 2, 256, 128), True, None), ((2, 1, 392, 128), False, 300),
+])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_mfma_backward_with_rotary_tables(shape, causal, valid, dt):
+    """The MFMA backward with Cayley tables (q, k rotated once into scratch, dq and dk rotated
+    back by R^T in the store epilogues) against the generic kernel with the same tables and the
+    float64 oracle on the rotated inputs."""
+    from algebraic_intelligence_amd import _lib
+    B, H, L, D = shape
+    scale = 1.0 if dt == torch.bfloat16 else 0.5
+    q, k, v = make_qkv(shape, dt, seed=sum(shape) + 17, scale=scale)
+    g = make_qkv(shape, dt, seed=sum(shape) + 18)[0]
+    c, s = O.cayley_tables(D, L + 3, freqs=10000.0 ** (-2.0 * np.arange(D // 2) / D))
+    c32, s32 = c.astype(np.float32), s.astype(np.float32)
+    rot = (torch.from_numpy(c32).to(DEV), torch.from_numpy(s32).to(DEV))
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, causal, valid, rot, 0, True)
+    mq, mk, mv = _bwd_flags(q, k, v, out, den, g, causal, valid, 0, rot)
+    gq, gk, gv = _bwd_flags(q, k, v, out, den, g, causal, valid, _lib.FLAG_GENERIC, rot)
+    cf, sf = c32[:L].astype(np.float64), s32[:L].astype(np.float64)
+    qr, kr = O.rotate_pairs(to_f64(q), cf, sf), O.rotate_pairs(to_f64(k), cf, sf)
+    rq, rk, rv = O.afa_backward(qr, kr, to_f64(v), to_f64(g), 0.5, causal, valid)
+    rq, rk = O.rotate_pairs(rq, cf, -sf), O.rotate_pairs(rk, cf, -sf)
+    for name, m, gen, r in (("dq", mq, gq, rq), ("dk", mk, gk, rk), ("dv", mv, gv, rv)):
+        assert torch.isfinite(m.float()).all(), name
+        e_g = normwise(to_f64(m), to_f64(gen))
+        e_r = normwise(to_f64(m), r)
+        print(f"rotary {shape} causal={causal} valid={valid} {dt} {name}: vs generic {e_g:.2e} vs fp64 {e_r:.2e}")
+        assert e_g <= 1e-2
         assert e_r <= 3e-2
 
 
