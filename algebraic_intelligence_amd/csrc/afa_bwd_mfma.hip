@@ -6,7 +6,9 @@
 //   ds = 8 scale r w (g_i . v_j - E_i);  dq_i += ds_ij k_j;  dk_j += ds_ij q_i;  dv_j += w_ij g_i,
 // with ds and w rounded to the input dtype as MFMA operands and fp32 accumulation.
 //
-// Three launches, no atomics:
+// Three launches (four with rotary tables), no atomics:
+//   * afa_bwd_mfma_rotate_kernel (rotary tables only): q and k rotated once into scratch; dq and
+//     dk are rotated back through R^T in the dQ / dK store epilogues;
 //   * afa_bwd_mfma_prep_kernel: E_i and 1/d_i per row into the workspace;
 //   * afa_bwd_mfma_dq_kernel (one lane per query, like the forward): S^T = K Q^T, dP^T = V g^T on
 //     MFMA, W and dS on the VALU, dQ^T += K^T dS^T with K^T read from the same LDS tile by
@@ -121,7 +123,7 @@ __device__ __forceinline__ float rho8r(float s, float& r) {
 
 }  // namespace
 
-// E_i = sum_d g_id out_id and 1/d_i per row (8 lanes per row).
+// E_i = sum_d g_id out_id and 1/d_i per row: 8 lanes per row, 16-byte chunks of g and out.
 template <int DT>
 __global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a) {
   const int64_t rows = (int64_t)a.B * a.H * a.L;
@@ -129,8 +131,15 @@ __global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a)
   const int sub = threadIdx.x & 7;
   float part = 0.f;
   if (row < rows) {
-    for (int d = sub; d < a.D; d += 8)
-      part += Elem<DT>::load(a.g, row * a.D + d) * Elem<DT>::load(a.out_in, row * a.D + d);
+    const unsigned short* gr = (const unsigned short*)a.g + row * a.D;
+    const unsigned short* orow = (const unsigned short*)a.out_in + row * a.D;
+    for (int c = sub; c < a.D / 8; c += 8) {
+      const u32x4_t gw = *(const u32x4_t*)(gr + c * 8);
+      const u32x4_t ow = *(const u32x4_t*)(orow + c * 8);
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        part += Elem<DT>::lo(gw[p]) * Elem<DT>::lo(ow[p]) + Elem<DT>::hi(gw[p]) * Elem<DT>::hi(ow[p]);
+    }
   }
   part += __shfl_xor(part, 1);
   part += __shfl_xor(part, 2);
@@ -174,7 +183,7 @@ __global__ __launch_bounds__(256) void afa_bwd_mfma_rotate_kernel(const GenArgs 
 
 // ------------------------------------------------------------------------------ dQ
 template <int DT, int D, bool EXACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, D == 64 ? 2 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : 2, D == 64 ? 3 : 2)))
 void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   constexpr int KT = 64;
   constexpr int NCK = D / 8;             // 16-byte chunks per row
