@@ -65,11 +65,33 @@ OACE_WORKLOADS = {
 }
 
 
+def warm_up(step, args):
+    """args.warmup untimed steps, then more until args.warmup_seconds have passed, so the timed
+    steps run at the clock the GPU holds under sustained load.  Returns (steps run, seconds)."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    for _ in range(args.warmup):
+        step()
+        n += 1
+    torch.cuda.synchronize()
+    while time.perf_counter() - t0 < args.warmup_seconds:
+        for _ in range(10):
+            step()
+        n += 10
+        torch.cuda.synchronize()
+    return n, round(time.perf_counter() - t0, 3)
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup-seconds", type=float, default=1.0,
+                    help="keep running untimed warmup steps until this much time has passed (the GPU "
+                         "raises its clock over the first tens of milliseconds of load)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--workload", default="c3",
@@ -149,9 +171,7 @@ def softmax_bench(args, dev):
         if r != 0:
             _lib.check(r, "asoftmax")
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm = warm_up(step, args)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(args.steps):
@@ -164,7 +184,8 @@ def softmax_bench(args, dev):
     print(json.dumps({
         "metric": f"A-Softmax {'VJP' if backward else 'forward'} HBM GB/s [{args.workload}]",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "warmup": args.warmup, "warmup_run": {"steps": warm[0], "seconds": warm[1]},
+        "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": dt_name,
         "data": "synthetic: x ~ 3 N(0,1), g ~ N(0,1) bf16, resident in HBM",
         "config": {"workload": workload, "rows": rows, "cols": cols, "bytes_per_step": nbytes},
@@ -218,9 +239,7 @@ def oace_bench(args, dev):
 
     fwd()
     step = train if backward == "step" else bwd if backward else fwd
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm = warm_up(step, args)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(args.steps):
@@ -238,7 +257,8 @@ def oace_bench(args, dev):
         "metric": f"fused Linear+OACE {dict([(False, 'forward'), (True, 'backward'), ('step', 'forward+backward')])[backward]} "
                   f"tokens/s (1 GPU) [{args.workload}]",
         "value": round(N / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_run": {"steps": warm[0], "seconds": warm[1]},
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: h, W ~ N(0,1) bf16, uniform targets, resident in HBM",
         "config": {"workload": workload, "rows": N, "d_model": d, "vocab": V, "w_layout": "(d_model, vocab)",
@@ -315,9 +335,7 @@ def main():
             if r != 0:
                 _lib.check(r, "afa_bwd")
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm = warm_up(step, args)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(args.steps):
@@ -343,7 +361,7 @@ def main():
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": args.warmup, "warmup_run": {"steps": warm[0], "seconds": warm[1]},
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -353,7 +371,10 @@ def main():
         "config": {"workload": workload, "batch": B, "heads": H, "seq_len": L, "head_dim": D,
                    "causal": causal, "sink_omega": 0.5, "flops_per_step": flops},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": traffic},
+                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": traffic,
+                     "duration_of": ("one afa_bwd call: every launch it makes" if backward else
+                                     "one afa_fwd call: every launch it makes (with rotary tables at "
+                                     "head_dim 64, the K rotation pre-pass and the attention kernel)")},
     }
     if args.workload != "c3":
         line["metric"] = METRIC.replace("at L=4096 D=64", f"at L={L} D={D}") + f" [{args.workload}]"
