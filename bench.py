@@ -31,6 +31,12 @@ PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "afa_fwd_c3_bf16_traffic.json")
 METRIC = "AFA fwd TFLOP/s + % bf16 MFMA peak at L=4096 D=64 (1 GPU); x vs host CPU ref"
 PEAK_FP32_TFLOPS = 157.3
+# VALU ceiling of the bf16/fp16 forward: each score costs 7.5 VALU lane-operations (the rho^8 chain,
+# row sum and bf16 pack: 120 VALU instructions per wave per 1024-score unit, counted in the
+# kernel's gfx950 ISA), issued at 16 lanes per cycle per SIMD for unpacked fp32 (the published
+# 157.3 TFLOP/s vector peak counts packed FMAs: 16 lanes x 2 x 2 FLOP), 1024 SIMDs at 2.4 GHz.
+VALU_OPS_PER_SCORE = 7.5
+VALU_LANE_OPS_PER_S = 16 * 1024 * 2.4e9
 # name -> (B, H, L, D, dtype, causal, rotary freqs: "c3" | "default" | None, backward, description)
 WORKLOADS = {
     "c3": (8, 12, 4096, 64, "bf16", True, "c3", False,
@@ -136,11 +142,25 @@ def cpu_baseline(q, k, v, rot, seconds):
                   nthreads=cores)
         elapsed += time.perf_counter() - t0
         heads += 1
+    # the same on one core, one head
+    t0 = time.perf_counter()
+    C.afa_fwd(qb[:1, :1], kb[:1, :1], vb[:1, :1], C.DT_BF16, 0.5, True, None, (rc, rs), block_q=128, block_k=128,
+              nthreads=1)
+    one = time.perf_counter() - t0
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {
         "value": round(per_head_flops * heads / elapsed / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
+        "cpu": model,
+        "one_core": {"value": round(per_head_flops / one / 1e12, 6), "unit": "TFLOP/s",
+                     "sample": f"1 (b,h) head, {one:.1f} s"},
         "sample": f"{heads} of {B * H} (b,h) heads of C3 (L={L}, D={D}, bf16, causal, AGO), "
                   f"{elapsed:.1f} s, C restatement oracle/afa_contract.c with OpenMP",
     }
@@ -272,7 +292,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the AFA path's multi-GPU sharding "
-                                   "is a design note (DESIGN.md), so --gpus must be 1"}))
+                                   "is a design note in the repository's documentation, so --gpus "
+                                   "must be 1"}))
         sys.exit(2)
 
     if args.copy_calibration:
@@ -336,14 +357,15 @@ def main():
                 _lib.check(r, "afa_bwd")
 
     warm = warm_up(step, args)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(args.steps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    ev[0].record(stream)
+    for i in range(args.steps):
         step()
-    end.record(stream)
+        ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    ms_total = start.elapsed_time(end)
+    ms_total = ev[0].elapsed_time(ev[-1])
     ms = ms_total / args.steps
+    ms_median = float(np.median([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
     flops = A.afa_flops(B, H, L, D, causal=causal) // 4 * (10 if backward else 4)
     tflops = flops / (ms * 1e-3) / 1e12
     if not torch.isfinite(out.float()).all():
@@ -363,6 +385,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup, "warmup_run": {"steps": warm[0], "seconds": warm[1]},
         "ms_per_step": round(ms, 5),
+        "ms_per_step_median": round(ms_median, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -376,6 +399,13 @@ def main():
                                      "one afa_fwd call: every launch it makes (with rotary tables at "
                                      "head_dim 64, the K rotation pre-pass and the attention kernel)")},
     }
+    if not backward and dt_name == "bf16":
+        # the score's VALU work against the same score's 4 D MFMA FLOPs
+        valu = VALU_LANE_OPS_PER_S / VALU_OPS_PER_SCORE * 4 * D / 1e12
+        both = 1.0 / (1.0 / peak + 1.0 / valu)
+        line["roofline"]["valu_ceiling"] = {
+            "tflops": round(valu, 1), "frac": round(tflops / valu, 4), "ops_per_score": VALU_OPS_PER_SCORE,
+            "mfma_plus_valu_no_overlap_tflops": round(both, 1), "frac_of_no_overlap": round(tflops / both, 4)}
     if args.workload != "c3":
         line["metric"] = METRIC.replace("at L=4096 D=64", f"at L={L} D={D}") + f" [{args.workload}]"
         if backward:
