@@ -163,22 +163,26 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     a.q_scale = 1.0f;
     a.w_unscale = 1.0f;
     const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, vlen);
-    if (head_dim == 64 && !(flags & AFA_FLAG_SIMPLE_SCHEDULE)) {
+    if ((head_dim == 64 || head_dim == 128) && !(flags & AFA_FLAG_SIMPLE_SCHEDULE)) {
       afa::FwdArgs b = a;
-      b.nqb = (int)((seq_len + 255) / 256);
-      // 256-query workgroups at two per CU; with fewer than that many workgroups the 32-query
-      // kernel (128-query workgroups, three per CU) fills the chip better
-      const bool small = (int64_t)b.B * b.H * b.nqb < 2 * (int64_t)cu_count();
+      // head_dim 64: 256-query workgroups at two per CU (afa_fwd_d64.hip) when there are at least
+      // that many workgroups; otherwise, and at head_dim 128, 128-query workgroups with several
+      // waves per SIMD (afa_fwd_pipe.hip)
+      const int64_t nwg256 = (int64_t)b.B * b.H * ((seq_len + 255) / 256);
+      const bool wide = head_dim == 64 && nwg256 >= 2 * (int64_t)cu_count();
+      // with rotary tables k is rotated once into stream-ordered scratch; without that scratch
+      // the single fused kernel below rotates at tile load
       void* krot = nullptr;
-      if (rot_cos != nullptr) krot = scratch_alloc(afa::d64_krot_bytes(b), s);
-      // without scratch for the rotated k, the single fused kernel below rotates at tile load
+      if (rot_cos != nullptr) krot = scratch_alloc(afa::krot_bytes(b, (int)head_dim), s);
       if (rot_cos == nullptr || krot != nullptr) {
-        hipError_t e;
-        if (small) {
-          e = krot != nullptr ? afa::d64_krot_launch(dtype, b, krot, s) : hipSuccess;
-          if (e == hipSuccess) e = afa::pipe_fwd_launch(dtype, 64, b, exact, s);
-        } else {
-          e = afa::d64_fwd_launch(dtype, b, exact, krot, s);
+        hipError_t e = krot != nullptr ? afa::krot_launch(dtype, (int)head_dim, b, krot, s) : hipSuccess;
+        if (e == hipSuccess) {
+          if (wide) {
+            b.nqb = (int)((seq_len + 255) / 256);
+            e = afa::d64_fwd_launch(dtype, b, exact, s);
+          } else {
+            e = afa::pipe_fwd_launch(dtype, (int)head_dim, b, exact, s);
+          }
         }
         if (krot != nullptr) {
           hipError_t e2 = hipFreeAsync(krot, s);
@@ -187,8 +191,6 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
         return hip_status(e);
       }
     }
-    if (head_dim == 128 && rot_cos == nullptr && !(flags & AFA_FLAG_SIMPLE_SCHEDULE))
-      return hip_status(afa::pipe_fwd_launch(dtype, 128, a, exact, s));
     return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
   }
   if (dtype == AFA_F32 && afa::f32_fwd_supported((int)head_dim) &&

@@ -86,25 +86,26 @@ __device__ __forceinline__ float tree16(const float (&p)[16]) {
 // lgkmcnt at their no-wait maxima).
 __host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
-// Cayley rotation of K, once per call: y (contiguous B, H, L, 64) = rotate(x) in fp32 with the
-// (L, 32) fp32 tables, rounded once to the element type -- the values the fused loader would
-// produce (rot4 with scale 1).  Grid (ceil(L / 64), B * H); each thread rotates 2 of the 8
-// 16-byte chunks of one key row (rows r and r + 32 of a 64-row block).
-template <int DT>
+// Cayley rotation of K, once per call: y (contiguous B, H, L, D) = rotate(x) in fp32 with the
+// (L, D/2) fp32 tables, rounded once to the element type -- the values the fused loaders would
+// produce (rot4 with scale 1).  Grid (ceil(L / 64), B * H); a block rotates 64 key rows, each
+// thread D/32 of their 16-byte chunks (chunk e = tid + 256 i: row e / (D/8), chunk e % (D/8)).
+template <int DT, int D>
 __global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y) {
+  constexpr int CH = D / 8;
   const int bh = blockIdx.y;
   const int b = bh / a.H, h = bh % a.H;
-  const int ch = threadIdx.x & 7;
-  const unsigned short* xb = (const unsigned short*)a.k + b * a.k_b + h * a.k_h + ch * 8;
-  unsigned short* yb = y + (int64_t)bh * a.L * 64 + ch * 8;
+  const unsigned short* xb = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
+  unsigned short* yb = y + (int64_t)bh * a.L * D;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int l = blockIdx.x * 64 + (threadIdx.x >> 3) + 32 * i;
+  for (int i = 0; i < 64 * CH / 256; ++i) {
+    const int e = threadIdx.x + 256 * i;
+    const int l = blockIdx.x * 64 + e / CH, ch = e % CH;
     if (l < a.L) {
-      const u32x4_t w = *(const u32x4_t*)(xb + (int64_t)l * a.k_l);
-      const f32x4_t cc = *(const f32x4_t*)(a.rc + l * 32 + ch * 4);
-      const f32x4_t ss = *(const f32x4_t*)(a.rs + l * 32 + ch * 4);
-      *(u32x4_t*)(yb + (int64_t)l * 64) = rot4<DT>(w, cc, ss, 1.0f);
+      const u32x4_t w = *(const u32x4_t*)(xb + (int64_t)l * a.k_l + ch * 8);
+      const f32x4_t cc = *(const f32x4_t*)(a.rc + (int64_t)l * (D / 2) + ch * 4);
+      const f32x4_t ss = *(const f32x4_t*)(a.rs + (int64_t)l * (D / 2) + ch * 4);
+      *(u32x4_t*)(yb + (int64_t)l * D + ch * 8) = rot4<DT>(w, cc, ss, 1.0f);
     }
   }
 }
@@ -370,32 +371,34 @@ static hipError_t launch_d64(const FwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-size_t d64_krot_bytes(const FwdArgs& a) { return (size_t)a.B * a.H * a.L * 64 * 2; }
+size_t krot_bytes(const FwdArgs& a, int head_dim) { return (size_t)a.B * a.H * a.L * head_dim * 2; }
 
-hipError_t d64_krot_launch(int dtype, FwdArgs& a, void* krot, hipStream_t stream) {
-  if (krot == nullptr) return hipErrorInvalidValue;
+template <int D>
+static void krot_launch_d(int dtype, const FwdArgs& a, void* krot, hipStream_t stream) {
   const dim3 grid((unsigned)((a.L + 63) / 64), (unsigned)(a.B * a.H));
   if (dtype == AFA_BF16)
-    hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
   else
-    hipLaunchKernelGGL((afa_krot_kernel<AFA_F16>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_F16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+}
+
+hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, hipStream_t stream) {
+  if (krot == nullptr || (head_dim != 64 && head_dim != 128)) return hipErrorInvalidValue;
+  if (head_dim == 64) krot_launch_d<64>(dtype, a, krot, stream);
+  else krot_launch_d<128>(dtype, a, krot, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   a.k = krot;
-  a.k_l = 64;
-  a.k_h = (int64_t)a.L * 64;
-  a.k_b = (int64_t)a.H * a.L * 64;
+  a.k_l = head_dim;
+  a.k_h = (int64_t)a.L * head_dim;
+  a.k_b = (int64_t)a.H * a.L * head_dim;
   return hipSuccess;
 }
 
-hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream) {
+hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream) {
   a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
   a.w_unscale = 1.0f;
   const bool rot = a.rc != nullptr;
-  if (rot) {
-    hipError_t e = d64_krot_launch(dtype, a, krot, stream);
-    if (e != hipSuccess) return e;
-  }
   if (dtype == AFA_BF16) {
     if (exact) return rot ? launch_d64<AFA_BF16, true, true>(a, stream) : launch_d64<AFA_BF16, true, false>(a, stream);
     return rot ? launch_d64<AFA_BF16, false, true>(a, stream) : launch_d64<AFA_BF16, false, false>(a, stream);

@@ -52,12 +52,13 @@ struct GenArgs {
 bool mfma_fwd_supported(int dtype, int head_dim);
 int mfma_fwd_queries_per_block(int head_dim);
 hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
-// Software-pipelined head_dim-64 kernel (afa_fwd_d64.hip); 256 queries per workgroup.  With
-// rotary tables it first rotates k into `krot` (d64_krot_bytes(a) bytes of device memory).
-size_t d64_krot_bytes(const FwdArgs& a);
-hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, void* krot, hipStream_t stream);
-// Rotates k once into `krot` (d64_krot_bytes(a) bytes) and points a's k at it (head_dim 64).
-hipError_t d64_krot_launch(int dtype, FwdArgs& a, void* krot, hipStream_t stream);
+// K rotated once per call (afa_krot_kernel, head_dim 64 or 128) into `krot` (krot_bytes bytes,
+// contiguous B, H, L, D); a's k then points at it.
+size_t krot_bytes(const FwdArgs& a, int head_dim);
+hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, hipStream_t stream);
+// Software-pipelined head_dim-64 kernel (afa_fwd_d64.hip); 256 queries per workgroup.  q is
+// rotated at load when a.rc is set; k must arrive rotated (krot_launch).
+hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);
 // 32 queries per wave, several waves per SIMD (afa_fwd_pipe.hip): head_dim 64 or 128, 128
 // queries per workgroup; q is rotated at load when a.rc is set, k must arrive rotated.
 hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);

@@ -65,8 +65,8 @@ int afa_version(void);
  * rot_cos/rot_sin (nullable, both or neither): Cayley rotary tables (rot_len, head_dim/2),
  * fp32 (fp64 for AFA_F64); q and k rows at position i are rotated by row i (fusing
  * _rotate_tensor, src/attention.py:142-152, as called from src/model.py:262-264): q when the
- * kernel loads it, k at tile load, except on the bf16/fp16 head_dim-64 path, where k is
- * rotated once per call into batch*heads*seq_len*64 elements of stream-ordered scratch
+ * kernel loads it, k at tile load, except on the bf16/fp16 head_dim 64 and 128 paths, where k
+ * is rotated once per call into batch*heads*seq_len*head_dim elements of stream-ordered scratch
  * (hipMallocAsync, freed on `stream` before the call returns; if that allocation fails the
  * fully fused kernel runs instead).  AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel.
  */

@@ -208,6 +208,13 @@ def test_generic_head_dims(D):
     assert normwise(to_f64(y), ref) <= 1e-5
 
 
+def _ulp_tol(dt):
+    """Bound for max|y - ref| / max|ref| between two outputs that are each rounded to dt after fp32
+    accumulation in different orders: one rounding flip of an element in the top binade costs up
+    to one ulp, 2^-7 of max|ref| in bf16 (7 explicit mantissa bits) and 2^-10 in fp16."""
+    return 8e-3 if dt == torch.bfloat16 else 4e-3
+
+
 def _cu_count():
     return torch.cuda.get_device_properties(0).multi_processor_count
 
@@ -237,14 +244,15 @@ def test_pipelined_d64_edge_shapes(shape, causal, valid, rot, dt, wide):
     a, da = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
     b, db = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_SIMPLE_SCHEDULE)
     assert np.isfinite(to_f64(a)).all()
-    assert normwise(to_f64(a), to_f64(b)) <= 4e-3
+    tol = _ulp_tol(dt)
+    assert normwise(to_f64(a), to_f64(b)) <= tol
     if wide:
         assert torch.equal(a, a[:, :H].repeat(1, reps, 1, 1))
         assert torch.equal(da, da[:, :H].repeat(1, reps, 1, 1))
         a, da = a[:, :H], da[:, :H]
     e_c = normwise(to_f64(a), c_out)
     print(f"d64 {shape} causal={causal} valid={valid} rot={rot} {dt} wide={wide} (x{reps}): vs contract {e_c:.2e}")
-    assert e_c <= 4e-3
+    assert e_c <= tol
     assert normwise(to_f64(da), c_den) <= 1e-5
 
 
@@ -291,22 +299,26 @@ def test_fp32_strided_model_layout():
     assert torch.equal(y_view, y_cont)
 
 
-@pytest.mark.parametrize("shape,causal,valid", [
-    ((1, 1, 1, 128), True, None), ((1, 1, 32, 128), False, None), ((2, 3, 96, 128), True, None),
-    ((1, 2, 300, 128), True, None), ((1, 2, 300, 128), False, 257), ((3, 5, 513, 128), True, 400),
-    ((1, 1, 1024, 128), False, None), ((2, 4, 1000, 128), True, None),
+@pytest.mark.parametrize("shape,causal,valid,rot", [
+    ((1, 1, 1, 128), True, None, False), ((1, 1, 32, 128), False, None, True), ((2, 3, 96, 128), True, None, False),
+    ((1, 2, 300, 128), True, None, True), ((1, 2, 300, 128), False, 257, False), ((3, 5, 513, 128), True, 400, True),
+    ((1, 1, 1024, 128), False, None, False), ((2, 4, 1000, 128), True, None, True),
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-def test_pipelined_d128_edge_shapes(shape, causal, valid, dt):
-    """The head_dim-128 kernel (afa_fwd_pipe.hip) against the simple MFMA kernel and the C
-    contract on ragged and tiny lengths, valid_len tails and odd head counts."""
+def test_pipelined_d128_edge_shapes(shape, causal, valid, rot, dt):
+    """The head_dim-128 kernel (afa_fwd_pipe.hip; with Cayley tables after the K rotation
+    pre-pass, q rotated at load) against the simple MFMA kernel (which rotates at tile load) and
+    the C contract on ragged and tiny lengths, valid_len tails and odd head counts."""
+    D, L = shape[3], shape[2]
     scale = 1.0 if dt == torch.bfloat16 else 0.3
     q, k, v = make_qkv(shape, dt, seed=sum(shape) + 1, scale=scale)
-    a, da = _fwd(q, k, v, causal=causal, valid=valid)
-    b, db = _fwd(q, k, v, causal=causal, valid=valid, flags=_lib.FLAG_SIMPLE_SCHEDULE)
-    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid)
+    rotary = A.build_cayley_rotary_matrix(D, L, freqs=_c3_freqs(D)) if rot else None
+    a, da = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
+    b, db = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_SIMPLE_SCHEDULE)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid, rotary=rotary)
     assert np.isfinite(to_f64(a)).all()
     e_s, e_c = normwise(to_f64(a), to_f64(b)), normwise(to_f64(a), c_out)
-    print(f"d128 {shape} causal={causal} valid={valid} {dt}: vs simple {e_s:.2e} vs contract {e_c:.2e}")
-    assert e_s <= 4e-3 and e_c <= 4e-3
+    print(f"d128 {shape} causal={causal} valid={valid} rot={rot} {dt}: vs simple {e_s:.2e} vs contract {e_c:.2e}")
+    tol = _ulp_tol(dt)
+    assert e_s <= tol and e_c <= tol
     assert normwise(to_f64(da), c_den) <= 1e-5
