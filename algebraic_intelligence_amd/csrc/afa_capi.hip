@@ -137,8 +137,11 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   const Strides st = resolve_strides(strides, heads, seq_len, head_dim);
   hipStream_t s = (hipStream_t)stream;
 
-  bool use_mfma = afa::mfma_fwd_supported(dtype, (int)head_dim) && !(flags & AFA_FLAG_GENERIC) &&
-                  !(flags & AFA_FLAG_EXACT_REF);
+  // bf16/fp16 matrix-core kernels: the fully fused one (afa_fwd_mfma.hip, head_dim 64 and 128)
+  // and the pipelined ones (head_dim 32, 48, 64, 96, 128)
+  const bool fused_ok = afa::mfma_fwd_supported(dtype, (int)head_dim);
+  const bool pipe_ok = afa::pipe_fwd_supported(dtype, (int)head_dim);
+  bool use_mfma = (fused_ok || pipe_ok) && !(flags & AFA_FLAG_GENERIC) && !(flags & AFA_FLAG_EXACT_REF);
   if (use_mfma) {
     // 16-byte vector loads/stores: 8-element aligned row strides and 16-byte aligned bases.
     for (int i = 0; i < 12; ++i)
@@ -147,7 +150,7 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     if (rot_cos != nullptr && (!aligned16(rot_cos) || !aligned16(rot_sin))) use_mfma = false;
   }
   if (use_mfma) {
-    afa::FwdArgs a;
+    afa::FwdArgs a = {};
     a.q = q; a.k = k; a.v = v; a.out = out; a.denom = (float*)denom;
     a.rc = (const float*)rot_cos; a.rs = (const float*)rot_sin;
     a.q_b = st.v[0]; a.q_h = st.v[1]; a.q_l = st.v[2];
@@ -157,21 +160,21 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len;
     a.valid_len = vlen;
     a.causal = causal ? 1 : 0;
-    const int qpb = afa::mfma_fwd_queries_per_block((int)head_dim);
-    a.nqb = (int)((seq_len + qpb - 1) / qpb);
     a.omega = (float)sink_omega;
     a.q_scale = 1.0f;
     a.w_unscale = 1.0f;
+    a.s_mult = 1.0f;
     const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, vlen);
-    if ((head_dim == 64 || head_dim == 128) && !(flags & AFA_FLAG_SIMPLE_SCHEDULE)) {
+    // AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel where it exists
+    if (pipe_ok && !(fused_ok && (flags & AFA_FLAG_SIMPLE_SCHEDULE))) {
       afa::FwdArgs b = a;
       // head_dim 64: 256-query workgroups at two per CU (afa_fwd_d64.hip) when there are at least
-      // that many workgroups; otherwise, and at head_dim 128, 128-query workgroups with several
-      // waves per SIMD (afa_fwd_pipe.hip)
+      // that many workgroups; otherwise, and at the other head dims, 128-query workgroups with
+      // several waves per SIMD (afa_fwd_pipe.hip)
       const int64_t nwg256 = (int64_t)b.B * b.H * ((seq_len + 255) / 256);
       const bool wide = head_dim == 64 && nwg256 >= 2 * (int64_t)cu_count();
       // with rotary tables k is rotated once into stream-ordered scratch; without that scratch
-      // the single fused kernel below rotates at tile load
+      // the fully fused kernel below (head_dim 64, 128) or the generic one rotates at tile load
       void* krot = nullptr;
       if (rot_cos != nullptr) krot = scratch_alloc(afa::krot_bytes(b, (int)head_dim), s);
       if (rot_cos == nullptr || krot != nullptr) {
@@ -191,7 +194,11 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
         return hip_status(e);
       }
     }
-    return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
+    if (fused_ok) {
+      const int qpb = afa::mfma_fwd_queries_per_block((int)head_dim);
+      a.nqb = (int)((seq_len + qpb - 1) / qpb);
+      return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
+    }
   }
   if (dtype == AFA_F32 && afa::f32_fwd_supported((int)head_dim) &&
       !(flags & (AFA_FLAG_GENERIC | AFA_FLAG_EXACT_REF))) {

@@ -88,8 +88,8 @@ __host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 
 
 // Cayley rotation of K, once per call: y (contiguous B, H, L, D) = rotate(x) in fp32 with the
 // (L, D/2) fp32 tables, rounded once to the element type -- the values the fused loaders would
-// produce (rot4 with scale 1).  Grid (ceil(L / 64), B * H); a block rotates 64 key rows, each
-// thread D/32 of their 16-byte chunks (chunk e = tid + 256 i: row e / (D/8), chunk e % (D/8)).
+// produce (rot4 with scale 1).  Grid (ceil(L / 64), B * H); a block rotates 64 key rows, thread
+// slot e = tid + 256 i covering row e / (D/8), 16-byte chunk e % (D/8).
 template <int DT, int D>
 __global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y) {
   constexpr int CH = D / 8;
@@ -98,10 +98,10 @@ __global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned
   const unsigned short* xb = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   unsigned short* yb = y + (int64_t)bh * a.L * D;
 #pragma unroll
-  for (int i = 0; i < 64 * CH / 256; ++i) {
+  for (int i = 0; i < (64 * CH + 255) / 256; ++i) {
     const int e = threadIdx.x + 256 * i;
     const int l = blockIdx.x * 64 + e / CH, ch = e % CH;
-    if (l < a.L) {
+    if (e < 64 * CH && l < a.L) {
       const u32x4_t w = *(const u32x4_t*)(xb + (int64_t)l * a.k_l + ch * 8);
       const f32x4_t cc = *(const f32x4_t*)(a.rc + (int64_t)l * (D / 2) + ch * 4);
       const f32x4_t ss = *(const f32x4_t*)(a.rs + (int64_t)l * (D / 2) + ch * 4);
@@ -383,9 +383,15 @@ static void krot_launch_d(int dtype, const FwdArgs& a, void* krot, hipStream_t s
 }
 
 hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, hipStream_t stream) {
-  if (krot == nullptr || (head_dim != 64 && head_dim != 128)) return hipErrorInvalidValue;
-  if (head_dim == 64) krot_launch_d<64>(dtype, a, krot, stream);
-  else krot_launch_d<128>(dtype, a, krot, stream);
+  if (krot == nullptr) return hipErrorInvalidValue;
+  switch (head_dim) {
+    case 32: krot_launch_d<32>(dtype, a, krot, stream); break;
+    case 48: krot_launch_d<48>(dtype, a, krot, stream); break;
+    case 64: krot_launch_d<64>(dtype, a, krot, stream); break;
+    case 96: krot_launch_d<96>(dtype, a, krot, stream); break;
+    case 128: krot_launch_d<128>(dtype, a, krot, stream); break;
+    default: return hipErrorInvalidValue;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   a.k = krot;

@@ -21,7 +21,14 @@
 //     2^-4 sqrt(2): 2^-4 is folded into q exactly, and sqrt(2) is either evaluated inside
 //     (rho/sqrt 2)^8 = rho^8/16 (bf16 fast path: weights and sink carry 1/16) or formed
 //     explicitly (two-branch path, fp16);
-//   * masks only on units that cross the causal diagonal or valid_len; workgroups heaviest first.
+//   * masks only on units that cross the causal diagonal or valid_len; workgroups heaviest first;
+//   * head_dim 32, 48 and 96 run as 64, 64 and 128: the padding chunks of every LDS row are
+//     loaded from a zero chunk in device memory (so every lane of every direct load is active and
+//     the per-tile load counts stay exact), q's padding features are zero, and only the head_dim
+//     output features are stored.  1/sqrt(D) is a power of two folded into q exactly times an
+//     fp32 factor applied to the score: s = (q 2^-k . k) * (fl(1/sqrt D) 2^k) rounds like the
+//     reference's (q . k) * fl(1/sqrt D).
+#include <cmath>
 #include <type_traits>
 
 #include "afa_common.h"
@@ -90,32 +97,40 @@ __device__ __forceinline__ int v_swizzle(int r, int c) {
   else return c ^ (((r >> 1) & 1) << 2);
 }
 
-template <int D>
+template <int DP>
 struct PipeShape {
   static constexpr int NB = 4;                  // ring of tile buffers
-  static constexpr int WAVES_PER_EU = D == 128 ? 2 : 3;
+  static constexpr int WAVES_PER_EU = DP == 128 ? 2 : 3;
 };
+
+constexpr int padded_dim(int d) { return d <= 64 ? 64 : 128; }
 
 }  // namespace
 
+// Source of the padding chunks of LDS rows (head_dim 32, 48, 96).
+__device__ __attribute__((aligned(16))) unsigned int afa_pipe_zero_chunk[4];
+
 // SM: 0 = s as formed (q carries 1/sqrt(D) exactly, D = 64);
 //     1 = s = sqrt(2) x evaluated as (rho/sqrt 2)^8 = rho^8/16 (weights and sink carry 1/16);
-//     2 = s = sqrt(2) x formed explicitly.
+//     2 = s = a.s_mult x formed explicitly.
 template <int D, int DT, bool EXACT, int SM, bool ROT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PipeShape<D>::WAVES_PER_EU,
-                                                                     PipeShape<D>::WAVES_PER_EU)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PipeShape<padded_dim(D)>::WAVES_PER_EU,
+                                                                     PipeShape<padded_dim(D)>::WAVES_PER_EU)))
 void afa_fwd_pipe_kernel(const FwdArgs a) {
+  constexpr int DP = padded_dim(D);      // LDS row and MFMA width
   constexpr int KT = 32;                 // keys per tile = one unit
-  constexpr int NB = PipeShape<D>::NB;
-  constexpr int CH = D / 8;              // 16-byte chunks per row
+  constexpr int NB = PipeShape<DP>::NB;
+  constexpr int CH = DP / 8;             // 16-byte chunks per LDS row
+  constexpr int CHD = D / 8;             // chunks that hold data
   constexpr int LPT = KT * CH / 256;     // direct loads per thread per tile, each of K and V
   constexpr int LOADS = 2 * LPT;
-  constexpr int NK = D / 16;             // 16-feature MFMA steps of S
-  constexpr int NDB = D / 32;            // 32-feature output blocks
+  constexpr int NK = DP / 16;            // 16-feature MFMA steps of S
+  constexpr int NDB = DP / 32;           // 32-feature output blocks
+  static_assert(D % 16 == 0 && D <= DP, "head_dim");
   static_assert(LPT >= 1 && KT * CH % 256 == 0, "tile loader shape");
   static_assert(NB == 4, "the waits below assume at most one tile in flight beyond the next");
-  __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * D];
-  __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * D];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * DP];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * DP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -141,8 +156,8 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
 #pragma unroll
   for (int kc = 0; kc < NK; ++kc) {
     u32x4_t w = {0u, 0u, 0u, 0u};
-    if (qi < L) {
-      const int d0 = kc * 16 + 8 * g;
+    const int d0 = kc * 16 + 8 * g;
+    if (qi < L && d0 < D) {
       const float* cc = ROT ? a.rc + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
       const float* ss = ROT ? a.rs + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
       w = q_chunk<DT, ROT>(*(const u32x4_t*)(qp + (int64_t)qi * a.q_l + d0), cc, ss, a.q_scale);
@@ -158,17 +173,21 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
     for (int i = 0; i < LPT; ++i) {
       const int s = tid + 256 * i, r = s / CH, pc = s % CH;
       const int key = min(t * KT + r, L - 1);  // rows past L: finite data, masked
-      const int lk = pc ^ (r & 7), lv = v_swizzle<D>(r, pc);
-      __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + lk * 8),
-                                       (void*)(kd + (256 * i + wave * 64) * 8), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lv * 8),
-                                       (void*)(vd + (256 * i + wave * 64) * 8), 16, 0, 0);
+      const int lk = pc ^ (r & 7), lv = v_swizzle<DP>(r, pc);
+      const void* ks = (const void*)(kp + (int64_t)key * a.k_l + lk * 8);
+      const void* vs = (const void*)(vp + (int64_t)key * a.v_l + lv * 8);
+      if constexpr (CHD < CH) {
+        if (lk >= CHD) ks = (const void*)afa_pipe_zero_chunk;
+        if (lv >= CHD) vs = (const void*)afa_pipe_zero_chunk;
+      }
+      __builtin_amdgcn_global_load_lds(ks, (void*)(kd + (256 * i + wave * 64) * 8), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vs, (void*)(vd + (256 * i + wave * 64) * 8), 16, 0, 0);
     }
   };
   u32x4_t kf[NK];
   u32x4_t vf[NDB][2];
   auto read_kf = [&](int u) {
-    const unsigned short* base = &lds_k[u % NB][l32 * D];
+    const unsigned short* base = &lds_k[u % NB][l32 * DP];
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & 7)) * 8));
   };
@@ -183,7 +202,7 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
         for (int hh = 0; hh < 2; ++hh) {
           const int row = kk * 16 + hh * 8 + 4 * g + (l16 >> 2);
           const int col = db * 32 + m16 * 16 + 4 * (l16 & 3);
-          const unsigned short* p = tile + row * D + v_swizzle<D>(row, col >> 3) * 8 + (col & 7);
+          const unsigned short* p = tile + row * DP + v_swizzle<DP>(row, col >> 3) * 8 + (col & 7);
           const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
           const u32x2_t w = __builtin_bit_cast(u32x2_t, v);
           f[2 * hh] = w[0];
@@ -229,7 +248,7 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
     float p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float x = SM == 2 ? scur[r] * 1.41421356237309515f : scur[r];
+      const float x = SM == 2 ? scur[r] * a.s_mult : scur[r];
       if constexpr (EXACT) p[r] = rho8_exact(x);
       else if constexpr (SM == 1) p[r] = rho8_fast_half(x);
       else p[r] = rho8_fast(x);
@@ -277,10 +296,13 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        u32x2_t w;
-        w[0] = Elem<DT>::pack(o[db][r4 * 4 + 0] * inv, o[db][r4 * 4 + 1] * inv);
-        w[1] = Elem<DT>::pack(o[db][r4 * 4 + 2] * inv, o[db][r4 * 4 + 3] * inv);
-        *(u32x2_t*)(op + db * 32 + r4 * 8 + 4 * g) = w;
+        const int f = db * 32 + r4 * 8 + 4 * g;  // features f .. f+3 (D is a multiple of 16)
+        if (D == DP || f < D) {
+          u32x2_t w;
+          w[0] = Elem<DT>::pack(o[db][r4 * 4 + 0] * inv, o[db][r4 * 4 + 1] * inv);
+          w[1] = Elem<DT>::pack(o[db][r4 * 4 + 2] * inv, o[db][r4 * 4 + 3] * inv);
+          *(u32x2_t*)(op + f) = w;
+        }
       }
     if (a.denom != nullptr && g == 0) a.denom[(int64_t)bh * L + qi] = tot * a.w_unscale;
   }
@@ -300,22 +322,52 @@ hipError_t launch_pipe(const FwdArgs& a, hipStream_t st) {
 
 }  // namespace
 
+bool pipe_fwd_supported(int dtype, int head_dim) {
+  return (dtype == AFA_BF16 || dtype == AFA_F16) &&
+         (head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128);
+}
+
+namespace {
+
+// 1/sqrt(D) = 2^-k * c: q carries 2^-k exactly; the score factor c = fl(1/sqrt D) * 2^k
+// (exact scaling of the reference's fp32 constant).
+template <int D>
+hipError_t launch_scaled(int dtype, FwdArgs a, bool exact, int k, hipStream_t st) {
+  a.q_scale = std::ldexp(1.0f, -k);
+  a.s_mult = std::ldexp((float)(1.0 / std::sqrt((double)D)), k);
+  if (dtype == AFA_BF16) return exact ? launch_pipe<D, AFA_BF16, true, 2>(a, st) : launch_pipe<D, AFA_BF16, false, 2>(a, st);
+  return exact ? launch_pipe<D, AFA_F16, true, 2>(a, st) : launch_pipe<D, AFA_F16, false, 2>(a, st);
+}
+
+// 1/sqrt(D) = 2^-k sqrt(2) (D = 32, 128): bf16 fast path evaluates (rho/sqrt 2)^8 = rho^8/16
+template <int D>
+hipError_t launch_sqrt2(int dtype, FwdArgs a, bool exact, int k, hipStream_t st) {
+  if (dtype == AFA_BF16 && !exact) {
+    a.q_scale = std::ldexp(1.0f, -k);
+    a.omega *= 0.0625f;
+    a.w_unscale = 16.0f;
+    return launch_pipe<D, AFA_BF16, false, 1>(a, st);
+  }
+  return launch_scaled<D>(dtype, a, exact, k, st);
+}
+
+}  // namespace
+
 hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t st) {
   a.nqb = (a.L + 127) / 128;
   a.w_unscale = 1.0f;
-  if (head_dim == 64) {
-    a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
-    if (dtype == AFA_BF16) return exact ? launch_pipe<64, AFA_BF16, true, 0>(a, st) : launch_pipe<64, AFA_BF16, false, 0>(a, st);
-    return exact ? launch_pipe<64, AFA_F16, true, 0>(a, st) : launch_pipe<64, AFA_F16, false, 0>(a, st);
+  a.s_mult = 1.0f;
+  switch (head_dim) {
+    case 32: return launch_sqrt2<32>(dtype, a, exact, 3, st);
+    case 48: return launch_scaled<48>(dtype, a, exact, 3, st);
+    case 64:
+      a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
+      if (dtype == AFA_BF16) return exact ? launch_pipe<64, AFA_BF16, true, 0>(a, st) : launch_pipe<64, AFA_BF16, false, 0>(a, st);
+      return exact ? launch_pipe<64, AFA_F16, true, 0>(a, st) : launch_pipe<64, AFA_F16, false, 0>(a, st);
+    case 96: return launch_scaled<96>(dtype, a, exact, 4, st);
+    case 128: return launch_sqrt2<128>(dtype, a, exact, 4, st);
+    default: return hipErrorInvalidValue;
   }
-  a.q_scale = 0.0625f;  // 2^-4 of 1/sqrt(128), exact
-  if (dtype == AFA_BF16) {
-    if (exact) return launch_pipe<128, AFA_BF16, true, 2>(a, st);
-    a.omega *= 0.0625f;
-    a.w_unscale = 16.0f;
-    return launch_pipe<128, AFA_BF16, false, 1>(a, st);
-  }
-  return exact ? launch_pipe<128, AFA_F16, true, 2>(a, st) : launch_pipe<128, AFA_F16, false, 2>(a, st);
 }
 
 }  // namespace afa

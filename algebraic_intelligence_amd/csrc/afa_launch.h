@@ -23,6 +23,7 @@ struct FwdArgs {
   float q_scale;    // power of two folded into q
   float omega;      // sink_omega times the weight scale
   float w_unscale;  // denominator output = w_unscale * (D' + omega)
+  float s_mult;     // fp32 factor of the score after the q_scale fold (kernels that take one)
 };
 
 // Generic forward / backward (afa_generic.hip).
@@ -52,15 +53,17 @@ struct GenArgs {
 bool mfma_fwd_supported(int dtype, int head_dim);
 int mfma_fwd_queries_per_block(int head_dim);
 hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
-// K rotated once per call (afa_krot_kernel, head_dim 64 or 128) into `krot` (krot_bytes bytes,
-// contiguous B, H, L, D); a's k then points at it.
+// K rotated once per call (afa_krot_kernel, head_dim 32, 48, 64, 96 or 128) into `krot`
+// (krot_bytes bytes, contiguous B, H, L, D); a's k then points at it.
 size_t krot_bytes(const FwdArgs& a, int head_dim);
 hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, hipStream_t stream);
 // Software-pipelined head_dim-64 kernel (afa_fwd_d64.hip); 256 queries per workgroup.  q is
 // rotated at load when a.rc is set; k must arrive rotated (krot_launch).
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);
-// 32 queries per wave, several waves per SIMD (afa_fwd_pipe.hip): head_dim 64 or 128, 128
-// queries per workgroup; q is rotated at load when a.rc is set, k must arrive rotated.
+// 32 queries per wave, several waves per SIMD (afa_fwd_pipe.hip): head_dim 32, 48, 64, 96 or
+// 128 (rows zero-padded to 64 or 128 in LDS), 128 queries per workgroup; q is rotated at load
+// when a.rc is set, k must arrive rotated.
+bool pipe_fwd_supported(int dtype, int head_dim);
 hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
 
 // fp32 forward on the fp32 MFMA (afa_fwd_f32.hip): head_dim 32/64/128, V and out rows 16-byte

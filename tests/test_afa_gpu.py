@@ -256,6 +256,39 @@ def test_pipelined_d64_edge_shapes(shape, causal, valid, rot, dt, wide):
     assert normwise(to_f64(da), c_den) <= 1e-5
 
 
+@pytest.mark.parametrize("D", [32, 48, 96])
+@pytest.mark.parametrize("shape,causal,valid,rot", [
+    ((1, 1, 1), True, None, False), ((2, 3, 96), True, None, True), ((1, 2, 300), False, 257, True),
+    ((3, 5, 513), True, 400, False), ((2, 4, 1000), True, None, True),
+])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_padded_head_dims(D, shape, causal, valid, rot, dt):
+    """head_dim 32, 48 and 96 on the matrix-core kernel (rows zero-padded to 64 / 128 in LDS,
+    1/sqrt(D) split into a power of two on q and an fp32 factor on the score) against the
+    generic kernel, the C contract and the float64 oracle."""
+    B, H, L = shape
+    scale = 1.0 if dt == torch.bfloat16 else 0.4
+    q, k, v = make_qkv((B, H, L, D), dt, seed=D + L + 5, scale=scale)
+    rotary = A.build_cayley_rotary_matrix(D, L, freqs=_c3_freqs(D)) if rot else None
+    a, da = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
+    b, db = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_GENERIC)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid, rotary=rotary)
+    qr, kr = to_f64(q), to_f64(k)
+    if rot:
+        c64, s64 = rotary.c.double().cpu().numpy(), rotary.s.double().cpu().numpy()
+        qr, kr = O.rotate_pairs(qr, c64, s64), O.rotate_pairs(kr, c64, s64)
+    ref, dref = O.afa_forward(qr, kr, to_f64(v), 0.5, causal, valid, return_denominator=True)
+    assert np.isfinite(to_f64(a)).all()
+    e_g, e_c, e_r = normwise(to_f64(a), to_f64(b)), normwise(to_f64(a), c_out), normwise(to_f64(a), ref)
+    print(f"D={D} {shape} causal={causal} valid={valid} rot={rot} {dt}: vs generic {e_g:.2e} "
+          f"vs contract {e_c:.2e} vs fp64 {e_r:.2e}")
+    tol = _ulp_tol(dt)
+    assert e_g <= tol and e_c <= tol
+    assert e_r <= 2e-2
+    assert normwise(to_f64(da), c_den) <= 1e-5
+    assert normwise(to_f64(da), dref) <= 1e-2
+
+
 def test_device_lds_limit_reported():
     p = torch.cuda.get_device_properties(0)
     print("device", p.name, "sharedMemPerBlock", getattr(p, "shared_memory_per_block", None),
