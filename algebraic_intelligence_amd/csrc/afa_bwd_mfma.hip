@@ -21,8 +21,11 @@
 //
 // Tiles of 64 rows are loaded by direct global -> LDS loads into two buffers; rows are D
 // elements with 16-byte chunks XOR-swizzled by (row & 7) (conflict-free 32-row fragments).
-// 1/sqrt(D) is split into a power of two folded into the register-resident operand (exact) and,
-// for D = 128, a factor 1/sqrt(2) applied to the fp32 score (the same rounding as s * scale).
+// 1/sqrt(D) is split into 1/8 folded into the register-resident operand (exact) and the factor
+// 8 fl(1/sqrt D) applied to the fp32 score (the same rounding as s * scale; 1 at D = 64).
+// head_dim 32, 48 and 96 run as 64, 64 and 128: padding chunks of the LDS rows are direct-loaded
+// from a zero chunk in device memory, padding features of the register operands are zero, and
+// only the head_dim features of dq, dk, dv are stored.
 #include <algorithm>
 #include <type_traits>
 
@@ -90,6 +93,16 @@ __device__ __forceinline__ u32x4_t frag_tr(const unsigned short* tile, int r0, i
 
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
+constexpr int padded_dim(int d) { return d <= 64 ? 64 : 128; }
+
+// Score factor after the folded 1/8: 8 fl(1/sqrt D) (a compile-time constant at D = 64, 128).
+template <int D>
+__device__ __forceinline__ float score_factor(const GenArgs& a) {
+  if constexpr (D == 64) return 1.0f;
+  else if constexpr (D == 128) return 0.70710677f;
+  else return (float)(8.0 * a.scale);
+}
+
 // Rotate the gradients of features f .. f+3 (two (even, odd) pairs, accumulator elements
 // e0 .. e0+3 of one lane) back through R^T: (g0, g1) -> (c g0 + s g1, c g1 - s g0), with the
 // fp32 Cayley tables at `trow` = position * D/2 + f/2.
@@ -122,6 +135,9 @@ __device__ __forceinline__ float rho8r(float s, float& r) {
 }
 
 }  // namespace
+
+// Source of the padding chunks of LDS rows (head_dim 32, 48, 96).
+__device__ __attribute__((aligned(16))) unsigned int afa_bwd_zero_chunk[4];
 
 // E_i = sum_d g_id out_id and 1/d_i per row: 8 lanes per row, 16-byte chunks of g and out.
 template <int DT>
@@ -183,17 +199,19 @@ __global__ __launch_bounds__(256) void afa_bwd_mfma_rotate_kernel(const GenArgs 
 
 // ------------------------------------------------------------------------------ dQ
 template <int DT, int D, bool EXACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : 2, D == 64 ? 3 : 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(padded_dim(D) == 64 ? 3 : 2,
+                                                                     padded_dim(D) == 64 ? 3 : 2)))
 void afa_bwd_mfma_dq_kernel(const GenArgs a) {
+  constexpr int DP = padded_dim(D);     // LDS row and MFMA width
   constexpr int KT = 64;
-  constexpr int NCK = D / 8;             // 16-byte chunks per row
+  constexpr int NCK = DP / 8;            // 16-byte chunks per LDS row
   constexpr int CPT = KT * NCK / 256;    // chunks per thread per tile and tensor
-  constexpr int NKC = D / 16;
-  constexpr int NFB = D / 32;
-  constexpr float SQ = D == 64 ? 1.0f : 0.70710677f;  // score factor after the folded 1/8
-  constexpr float C8 = D == 64 ? 1.0f : 0.70710677f;  // 8 * scale
-  __shared__ __attribute__((aligned(16))) unsigned short lds_k[2][KT * D];
-  __shared__ __attribute__((aligned(16))) unsigned short lds_v[2][KT * D];
+  constexpr int NKC = DP / 16;
+  constexpr int NFB = DP / 32;
+  const float SQ = score_factor<D>(a);  // score factor after the folded 1/8
+  const float C8 = SQ;                  // 8 * scale
+  __shared__ __attribute__((aligned(16))) unsigned short lds_k[2][KT * DP];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_v[2][KT * DP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -221,7 +239,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
     u32x4_t z = {0u, 0u, 0u, 0u};
     qf[kc] = z;
     gf[kc] = z;
-    if (qi < L) {
+    if (qi < L && 16 * kc + 8 * g < D) {
       qf[kc] = bscale<DT>(*(const u32x4_t*)(qp + (int64_t)qi * D + 16 * kc + 8 * g), 0.125f);
       gf[kc] = *(const u32x4_t*)(gp + (int64_t)qi * D + 16 * kc + 8 * g);
     }
@@ -245,8 +263,13 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       const int lc = pc ^ (row & 7);
       unsigned short* kd = &lds_k[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* vd = &lds_v[t & 1][(256 * i + wave * 64) * 8];
-      __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * D + lc * 8), (void*)kd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * D + lc * 8), (void*)vd, 16, 0, 0);
+      const void* ks = (const void*)(kp + (int64_t)key * D + lc * 8);
+      const void* vs = (const void*)(vp + (int64_t)key * D + lc * 8);
+      if constexpr (D < DP) {
+        if (lc >= D / 8) ks = vs = (const void*)afa_bwd_zero_chunk;
+      }
+      __builtin_amdgcn_global_load_lds(ks, (void*)kd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vs, (void*)vd, 16, 0, 0);
     }
   };
 
@@ -270,9 +293,9 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
           P[e] = 0.f;
         }
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<D>(tk, rk, 2 * kc + g), qf[kc], S);
+        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tk, rk, 2 * kc + g), qf[kc], S);
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<D>(tv, rk, 2 * kc + g), gf[kc], P);
+        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<DP>(tv, rk, 2 * kc + g), gf[kc], P);
         const bool need_mask = (a.causal && n * 32 + 31 > q0_w) || n * 32 + 31 >= vlen || q0_w + 31 >= L;
         float ds[16];
 #pragma unroll
@@ -299,7 +322,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
         for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk)
-            dq[fb] = bmma<DT>(frag_tr<D>(tk, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dq[fb]);
+            dq[fb] = bmma<DT>(frag_tr<DP>(tk, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dq[fb]);
       }
     }
     __builtin_amdgcn_s_waitcnt(vm_only(0));
@@ -312,35 +335,41 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4)
-          unrotate4(dq[fb], 4 * r4, (const float*)a.rc, (const float*)a.rs,
-                    (int64_t)qi * (D / 2) + fb * 16 + r4 * 4 + 2 * g);
+          if (fb * 32 + r4 * 8 + 4 * g < D)
+            unrotate4(dq[fb], 4 * r4, (const float*)a.rc, (const float*)a.rs,
+                      (int64_t)qi * (D / 2) + fb * 16 + r4 * 4 + 2 * g);
     }
     unsigned short* op = (unsigned short*)a.out + base + (int64_t)qi * D;
 #pragma unroll
     for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        u32x2_t w;
-        w[0] = Elem<DT>::pack(dq[fb][4 * r4 + 0], dq[fb][4 * r4 + 1]);
-        w[1] = Elem<DT>::pack(dq[fb][4 * r4 + 2], dq[fb][4 * r4 + 3]);
-        *(u32x2_t*)(op + fb * 32 + r4 * 8 + 4 * g) = w;
+        const int f = fb * 32 + r4 * 8 + 4 * g;  // features f .. f+3 (D is a multiple of 16)
+        if (D == DP || f < D) {
+          u32x2_t w;
+          w[0] = Elem<DT>::pack(dq[fb][4 * r4 + 0], dq[fb][4 * r4 + 1]);
+          w[1] = Elem<DT>::pack(dq[fb][4 * r4 + 2], dq[fb][4 * r4 + 3]);
+          *(u32x2_t*)(op + f) = w;
+        }
       }
   }
 }
 
 // ------------------------------------------------------------------------------ dK, dV
 template <int DT, int D, bool EXACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1, D == 64 ? 2 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(padded_dim(D) == 64 ? 2 : 1,
+                                                                     padded_dim(D) == 64 ? 2 : 1)))
 void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
+  constexpr int DP = padded_dim(D);
   constexpr int QT = 64;
-  constexpr int NCK = D / 8;
+  constexpr int NCK = DP / 8;
   constexpr int CPT = QT * NCK / 256;
-  constexpr int NKC = D / 16;
-  constexpr int NFB = D / 32;
-  constexpr float SQ = D == 64 ? 1.0f : 0.70710677f;
-  constexpr float C8 = D == 64 ? 1.0f : 0.70710677f;
-  __shared__ __attribute__((aligned(16))) unsigned short lds_q[2][QT * D];
-  __shared__ __attribute__((aligned(16))) unsigned short lds_g[2][QT * D];
+  constexpr int NKC = DP / 16;
+  constexpr int NFB = DP / 32;
+  const float SQ = score_factor<D>(a);
+  const float C8 = SQ;
+  __shared__ __attribute__((aligned(16))) unsigned short lds_q[2][QT * DP];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_g[2][QT * DP];
   __shared__ __attribute__((aligned(16))) float lds_ei[2][2 * QT];  // E then 1/d of the tile's rows
 
   const int tid = threadIdx.x;
@@ -372,7 +401,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
     u32x4_t z = {0u, 0u, 0u, 0u};
     kf[kc] = z;
     vf[kc] = z;
-    if (kj < L) {
+    if (kj < L && 16 * kc + 8 * g < D) {
       kf[kc] = bscale<DT>(*(const u32x4_t*)(kp + (int64_t)kj * D + 16 * kc + 8 * g), 0.125f);
       vf[kc] = *(const u32x4_t*)(vp + (int64_t)kj * D + 16 * kc + 8 * g);
     }
@@ -395,8 +424,13 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       const int lc = pc ^ (row & 7);
       unsigned short* qd = &lds_q[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* gd = &lds_g[t & 1][(256 * i + wave * 64) * 8];
-      __builtin_amdgcn_global_load_lds((const void*)(qp + (int64_t)qrow * D + lc * 8), (void*)qd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(gp + (int64_t)qrow * D + lc * 8), (void*)gd, 16, 0, 0);
+      const void* qs = (const void*)(qp + (int64_t)qrow * D + lc * 8);
+      const void* gs = (const void*)(gp + (int64_t)qrow * D + lc * 8);
+      if constexpr (D < DP) {
+        if (lc >= D / 8) qs = gs = (const void*)afa_bwd_zero_chunk;
+      }
+      __builtin_amdgcn_global_load_lds(qs, (void*)qd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gs, (void*)gd, 16, 0, 0);
     }
     if (wave == 0 && lane < 32) {
       // 16 lanes of E, 16 of 1/d: 4 rows per lane (L % 4 == 0, so a chunk is either inside
@@ -430,9 +464,9 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
           P[e] = 0.f;
         }
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<D>(tq, rq, 2 * kc + g), kf[kc], S);
+        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<D>(tg, rq, 2 * kc + g), vf[kc], P);
+        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vf[kc], P);
         float w[16], ds[16];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
@@ -470,8 +504,8 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
         for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk) {
-            dv[fb] = bmma<DT>(frag_tr<D>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
-            dk[fb] = bmma<DT>(frag_tr<D>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
+            dv[fb] = bmma<DT>(frag_tr<DP>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
+            dk[fb] = bmma<DT>(frag_tr<DP>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
           }
       }
     }
@@ -485,8 +519,9 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4)
-          unrotate4(dk[fb], 4 * r4, (const float*)a.rc, (const float*)a.rs,
-                    (int64_t)kj * (D / 2) + fb * 16 + r4 * 4 + 2 * g);
+          if (fb * 32 + r4 * 8 + 4 * g < D)
+            unrotate4(dk[fb], 4 * r4, (const float*)a.rc, (const float*)a.rs,
+                      (int64_t)kj * (D / 2) + fb * 16 + r4 * 4 + 2 * g);
     }
     unsigned short* kout = (unsigned short*)a.dk + base + (int64_t)kj * D;
     unsigned short* vout = (unsigned short*)a.dv + base + (int64_t)kj * D;
@@ -494,21 +529,25 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
     for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        u32x2_t wk, wv;
-        wk[0] = Elem<DT>::pack(dk[fb][4 * r4 + 0], dk[fb][4 * r4 + 1]);
-        wk[1] = Elem<DT>::pack(dk[fb][4 * r4 + 2], dk[fb][4 * r4 + 3]);
-        wv[0] = Elem<DT>::pack(dv[fb][4 * r4 + 0], dv[fb][4 * r4 + 1]);
-        wv[1] = Elem<DT>::pack(dv[fb][4 * r4 + 2], dv[fb][4 * r4 + 3]);
-        *(u32x2_t*)(kout + fb * 32 + r4 * 8 + 4 * g) = wk;
-        *(u32x2_t*)(vout + fb * 32 + r4 * 8 + 4 * g) = wv;
+        const int f = fb * 32 + r4 * 8 + 4 * g;  // features f .. f+3 (D is a multiple of 16)
+        if (D == DP || f < D) {
+          u32x2_t wk, wv;
+          wk[0] = Elem<DT>::pack(dk[fb][4 * r4 + 0], dk[fb][4 * r4 + 1]);
+          wk[1] = Elem<DT>::pack(dk[fb][4 * r4 + 2], dk[fb][4 * r4 + 3]);
+          wv[0] = Elem<DT>::pack(dv[fb][4 * r4 + 0], dv[fb][4 * r4 + 1]);
+          wv[1] = Elem<DT>::pack(dv[fb][4 * r4 + 2], dv[fb][4 * r4 + 3]);
+          *(u32x2_t*)(kout + f) = wk;
+          *(u32x2_t*)(vout + f) = wv;
+        }
       }
   }
 }
 
 // ------------------------------------------------------------------------------ launcher
 bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len) {
-  return (dtype == AFA_BF16 || dtype == AFA_F16) && (head_dim == 64 || head_dim == 128) && seq_len >= 4 &&
-         seq_len % 4 == 0;
+  return (dtype == AFA_BF16 || dtype == AFA_F16) &&
+         (head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128) &&
+         seq_len >= 4 && seq_len % 4 == 0;
 }
 
 size_t mfma_bwd_rot_bytes(const GenArgs& a) { return (size_t)a.B * a.H * a.L * a.D * 2 * 2; }
@@ -533,10 +572,21 @@ static hipError_t bwd_launch(GenArgs a, void* rot_scratch, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int DT, int D>
+static hipError_t bwd_launch_e(const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st) {
+  return exact ? bwd_launch<DT, D, true>(a, rot_scratch, st) : bwd_launch<DT, D, false>(a, rot_scratch, st);
+}
+
 template <int DT>
 static hipError_t bwd_launch_dt(const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st) {
-  if (a.D == 64) return exact ? bwd_launch<DT, 64, true>(a, rot_scratch, st) : bwd_launch<DT, 64, false>(a, rot_scratch, st);
-  return exact ? bwd_launch<DT, 128, true>(a, rot_scratch, st) : bwd_launch<DT, 128, false>(a, rot_scratch, st);
+  switch (a.D) {
+    case 32: return bwd_launch_e<DT, 32>(a, exact, rot_scratch, st);
+    case 48: return bwd_launch_e<DT, 48>(a, exact, rot_scratch, st);
+    case 64: return bwd_launch_e<DT, 64>(a, exact, rot_scratch, st);
+    case 96: return bwd_launch_e<DT, 96>(a, exact, rot_scratch, st);
+    case 128: return bwd_launch_e<DT, 128>(a, exact, rot_scratch, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st) {

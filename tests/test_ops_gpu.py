@@ -126,12 +126,15 @@ def _bwd_flags(q, k, v, out, den, g, causal, valid, flags, rot=None):
 @pytest.mark.parametrize("shape,causal,valid", [
     ((1, 2, 256, 64), True, None), ((2, 3, 200, 64), False, None), ((1, 2, 1000, 64), True, 777),
     ((1, 1, 4, 64), True, None), ((1, 2, 256, 128), True, None), ((2, 1, 392, 128), False, 300),
-    ((1, 1, 128, 128), True, 61),
+    ((1, 1, 128, 128), True, 61), ((1, 2, 256, 32), True, None), ((2, 3, 200, 48), False, None),
+    ((1, 2, 300, 48), True, 257), ((1, 1, 8, 48), True, None), ((1, 2, 392, 96), True, None),
+    ((2, 1, 200, 96), False, 150),
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_mfma_backward_vs_generic_and_contract(shape, causal, valid, dt):
-    """The MFMA backward (bf16/fp16, head_dim 64/128) against the generic kernel (forced with
-    AFA_FLAG_GENERIC), the C contract restatement and the float64 oracle."""
+    """The MFMA backward (bf16/fp16, head_dim 64/128, and 32/48/96 padded to 64/128) against the
+    generic kernel (forced with AFA_FLAG_GENERIC), the C contract restatement and the float64
+    oracle."""
     from algebraic_intelligence_amd import _lib
     scale = 1.0 if dt == torch.bfloat16 else 0.5
     q, k, v = make_qkv(shape, dt, seed=sum(shape) + 7, scale=scale)
@@ -156,7 +159,8 @@ def test_mfma_backward_vs_generic_and_contract(shape, causal, valid, dt):
 
 @pytest.mark.parametrize("shape,causal,valid", [
     ((1, 2, 256, 64), True, None), ((2, 3, 200, 64), False, None), ((1, 2, 1000, 64), True, 777),
-    ((1, 2, 256, 128), True, None), ((2, 1, 392, 128), False, 300),
+    ((1, 2, 256, 128), True, None), ((2, 1, 392, 128), False, 300), ((1, 2, 200, 48), True, None),
+    ((1, 2, 300, 96), False, 257), ((1, 1, 128, 32), True, None),
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_mfma_backward_with_rotary_tables(shape, causal, valid, dt):
