@@ -31,6 +31,7 @@ PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "afa_fwd_c3_bf16_traffic.json")
 METRIC = "AFA fwd TFLOP/s + % bf16 MFMA peak at L=4096 D=64 (1 GPU); x vs host CPU ref"
 PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
 # VALU ceiling of the bf16/fp16 forward: each score costs 7.5 VALU lane-operations (the rho^8 chain,
 # row sum and bf16 pack: 120 VALU instructions per wave per 1024-score unit, counted in the
 # kernel's gfx950 ISA), issued at 16 lanes per cycle per SIMD for unpacked fp32 (the published
@@ -39,6 +40,7 @@ VALU_OPS_PER_SCORE = 7.5
 VALU_LANE_OPS_PER_S = 16 * 1024 * 2.4e9
 # name -> (B, H, L, D, dtype, causal, rotary freqs: "c3" | "default" | None, backward, description)
 WORKLOADS = {
+    "c1": (1, 4, 256, 64, "fp32", False, None, False, "C1: AFA forward, fp32, non-causal (latency-bound)"),
     "c3": (8, 12, 4096, 64, "bf16", True, "c3", False,
            "C3: AFA forward, causal, Cayley rotary fused in-kernel"),
     "c2": (4, 8, 2048, 64, "bf16", True, None, False, "C2: AFA forward, causal"),
@@ -368,9 +370,16 @@ def main():
     ms_median = float(np.median([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
     flops = A.afa_flops(B, H, L, D, causal=causal) // 4 * (10 if backward else 4)
     tflops = flops / (ms * 1e-3) / 1e12
+    # algorithmic HBM bytes: q, k, v in and out (forward); q, k, v, out, g in and dq, dk, dv out,
+    # plus d (backward); the fp32 Cayley tables when given
+    esz = 2 if dt_name == "bf16" else 4
+    tensors = 8 if backward else 4
+    nbytes = tensors * B * H * L * D * esz + (4 * B * H * L if backward else 0) + (4 * L * D if rot is not None else 0)
+    gbs = nbytes / (ms * 1e-3) / 1e9
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite output")
     peak = PEAK_BF16_TFLOPS if dt_name == "bf16" else PEAK_FP32_TFLOPS
+    hbm_bound = flops / nbytes < peak * 1e12 / (PEAK_HBM_GBS * 1e9)  # below the ridge point
 
     traffic = None
     if args.workload == "c3" and os.path.exists(TRAFFIC_FILE):
@@ -398,7 +407,13 @@ def main():
                      "duration_of": ("one afa_bwd call: every launch it makes" if backward else
                                      "one afa_fwd call: every launch it makes (with rotary tables at "
                                      "head_dim 64, the K rotation pre-pass and the attention kernel)")},
+        "hbm": {"algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1), "peak_gbs": PEAK_HBM_GBS,
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "flop_per_byte": round(flops / nbytes, 1)},
     }
+    if hbm_bound:
+        # arithmetic intensity below the ridge point: the HBM roofline bounds this configuration
+        line["roofline"].update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                 "frac": round(gbs / PEAK_HBM_GBS, 4)})
     if not backward and dt_name == "bf16":
         # the score's VALU work against the same score's 4 D MFMA FLOPs
         valu = VALU_LANE_OPS_PER_S / VALU_OPS_PER_SCORE * 4 * D / 1e12
