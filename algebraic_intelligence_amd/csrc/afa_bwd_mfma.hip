@@ -139,14 +139,25 @@ __device__ __forceinline__ float rho8r(float s, float& r) {
 // Source of the padding chunks of LDS rows (head_dim 32, 48, 96).
 __device__ __attribute__((aligned(16))) unsigned int afa_bwd_zero_chunk[4];
 
+// Rows of a head in the workspace: seq_len rounded up to 4, so that every 16-byte chunk of E or
+// 1/d lies inside one head (the dK/dV kernel loads them 4 rows at a time).
+__host__ __device__ constexpr int ws_rows(int L) { return (L + 3) & ~3; }
+
 // E_i = sum_d g_id out_id and 1/d_i per row: 8 lanes per row, 16-byte chunks of g and out.
+// Workspace layout: E at [bh * LP + i], 1/d at [B H LP + bh * LP + i], LP = ws_rows(L); the
+// padding rows hold zeros.
 template <int DT>
 __global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a) {
-  const int64_t rows = (int64_t)a.B * a.H * a.L;
-  const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int LP = ws_rows(a.L);
+  const int64_t prow = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);  // workspace row
+  const int64_t prows = (int64_t)a.B * a.H * LP;
+  const int64_t bh = prow / LP;
+  const int l = (int)(prow - bh * LP);
+  const int64_t row = bh * a.L + l;  // input row
+  const bool live = prow < prows && l < a.L;
   const int sub = threadIdx.x & 7;
   float part = 0.f;
-  if (row < rows) {
+  if (live) {
     const unsigned short* gr = (const unsigned short*)a.g + row * a.D;
     const unsigned short* orow = (const unsigned short*)a.out_in + row * a.D;
     for (int c = sub; c < a.D / 8; c += 8) {
@@ -160,9 +171,9 @@ __global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a)
   part += __shfl_xor(part, 1);
   part += __shfl_xor(part, 2);
   part += __shfl_xor(part, 4);
-  if (row < rows && sub == 0) {
-    ((float*)a.e_ws)[row] = part;
-    ((float*)a.e_ws)[rows + row] = 1.0f / ((const float*)a.dtot)[row];
+  if (prow < prows && sub == 0) {
+    ((float*)a.e_ws)[prow] = live ? part : 0.f;
+    ((float*)a.e_ws)[prows + prow] = live ? 1.0f / ((const float*)a.dtot)[row] : 0.f;
   }
 }
 
@@ -244,9 +255,10 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       gf[kc] = *(const u32x4_t*)(gp + (int64_t)qi * D + 16 * kc + 8 * g);
     }
   }
-  const int64_t rows = (int64_t)BH * L;
-  const float ei = qi < L ? ((const float*)a.e_ws)[(int64_t)bh * L + qi] : 0.f;
-  const float invd = qi < L ? ((const float*)a.e_ws)[rows + (int64_t)bh * L + qi] : 0.f;
+  const int LP = ws_rows(L);
+  const int64_t prows = (int64_t)BH * LP;
+  const float ei = qi < L ? ((const float*)a.e_ws)[(int64_t)bh * LP + qi] : 0.f;
+  const float invd = qi < L ? ((const float*)a.e_ws)[prows + (int64_t)bh * LP + qi] : 0.f;
 
   f32x16_t dq[NFB];
 #pragma unroll
@@ -391,9 +403,9 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   const unsigned short* kp = (const unsigned short*)a.k + base;
   const unsigned short* vp = (const unsigned short*)a.v + base;
   const unsigned short* gp = (const unsigned short*)a.g + base;
-  const int64_t rows = (int64_t)BH * L;
-  const float* ep = (const float*)a.e_ws + (int64_t)bh * L;
-  const float* ip = (const float*)a.e_ws + rows + (int64_t)bh * L;
+  const int LP = ws_rows(L);
+  const float* ep = (const float*)a.e_ws + (int64_t)bh * LP;
+  const float* ip = (const float*)a.e_ws + (int64_t)BH * LP + (int64_t)bh * LP;
 
   u32x4_t kf[NKC], vf[NKC];
 #pragma unroll
@@ -433,10 +445,10 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       __builtin_amdgcn_global_load_lds(gs, (void*)gd, 16, 0, 0);
     }
     if (wave == 0 && lane < 32) {
-      // 16 lanes of E, 16 of 1/d: 4 rows per lane (L % 4 == 0, so a chunk is either inside
-      // the sequence or past it); chunks past L re-read the last one (those rows are masked)
+      // 16 lanes of E, 16 of 1/d: 4 rows per lane (the head's LP rows are a whole number of
+      // chunks; rows in [L, LP) hold zeros); chunks past LP re-read the last one (masked rows)
       const int rr = t * QT + (lane & 15) * 4;
-      const int r0 = rr < L ? rr : L - 4;
+      const int r0 = rr < LP ? rr : LP - 4;
       const float* src = (lane < 16 ? ep : ip) + r0;
       __builtin_amdgcn_global_load_lds((const void*)src, (void*)&lds_ei[t & 1][0], 16, 0, 0);
     }
@@ -547,7 +559,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
 bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len) {
   return (dtype == AFA_BF16 || dtype == AFA_F16) &&
          (head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128) &&
-         seq_len >= 4 && seq_len % 4 == 0;
+         seq_len >= 1;
 }
 
 size_t mfma_bwd_rot_bytes(const GenArgs& a) { return (size_t)a.B * a.H * a.L * a.D * 2 * 2; }
@@ -565,7 +577,8 @@ static hipError_t bwd_launch(GenArgs a, void* rot_scratch, hipStream_t st) {
     a.q = qr;
     a.k = kr;
   }
-  hipLaunchKernelGGL((afa_bwd_mfma_prep_kernel<DT>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, st, a);
+  const int64_t prows = (int64_t)a.B * a.H * ws_rows(a.L);
+  hipLaunchKernelGGL((afa_bwd_mfma_prep_kernel<DT>), dim3((unsigned)((prows + 31) / 32)), dim3(256), 0, st, a);
   const int nb = a.B * a.H * ((a.L + 127) / 128);
   hipLaunchKernelGGL((afa_bwd_mfma_dq_kernel<DT, D, EXACT>), dim3(nb), dim3(256), 0, st, a);
   hipLaunchKernelGGL((afa_bwd_mfma_dkdv_kernel<DT, D, EXACT>), dim3(nb), dim3(256), 0, st, a);

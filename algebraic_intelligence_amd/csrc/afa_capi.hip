@@ -245,7 +245,9 @@ size_t afa_bwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t s
                               int64_t head_dim) {
   (void)head_dim;
   if (!valid_dtype(dtype) || batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
-  return (size_t)(batch * heads * seq_len) * acc_size(dtype) * 2;
+  // E and 1/d per row; each head's rows padded to a multiple of 4 (the matrix-core kernels load
+  // them in 16-byte chunks)
+  return (size_t)(batch * heads * ((seq_len + 3) / 4 * 4)) * acc_size(dtype) * 2;
 }
 
 int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,

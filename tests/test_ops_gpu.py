@@ -128,7 +128,8 @@ def _bwd_flags(q, k, v, out, den, g, causal, valid, flags, rot=None):
     ((1, 1, 4, 64), True, None), ((1, 2, 256, 128), True, None), ((2, 1, 392, 128), False, 300),
     ((1, 1, 128, 128), True, 61), ((1, 2, 256, 32), True, None), ((2, 3, 200, 48), False, None),
     ((1, 2, 300, 48), True, 257), ((1, 1, 8, 48), True, None), ((1, 2, 392, 96), True, None),
-    ((2, 1, 200, 96), False, 150),
+    ((2, 1, 200, 96), False, 150), ((1, 2, 257, 64), True, None), ((2, 1, 130, 128), False, 100),
+    ((1, 1, 1, 64), True, None), ((1, 3, 3, 48), False, None), ((1, 2, 1001, 96), True, 999),
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_mfma_backward_vs_generic_and_contract(shape, causal, valid, dt):
