@@ -298,7 +298,12 @@ int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     if (rot == nullptr) use_mfma = false;
   }
   const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, a.valid_len);
-  hipError_t e = use_mfma ? afa::mfma_bwd_launch(dtype, a, exact, rot, s) : afa::generic_bwd_launch(dtype, a, s);
+  // fp32: the fp32 matrix-core kernels (q and k rotated as they are staged)
+  const bool use_f32 = dtype == AFA_F32 && !(flags & AFA_FLAG_GENERIC) && aligned &&
+                       afa::f32_bwd_supported((int)head_dim);
+  hipError_t e = use_mfma  ? afa::mfma_bwd_launch(dtype, a, exact, rot, s)
+                 : use_f32 ? afa::f32_bwd_launch(a, s)
+                           : afa::generic_bwd_launch(dtype, a, s);
   if (rot != nullptr) {
     hipError_t e2 = hipFreeAsync(rot, s);
     if (e == hipSuccess) e = e2;

@@ -79,6 +79,10 @@ hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len);
 size_t mfma_bwd_rot_bytes(const GenArgs& a);
 hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st);
+// fp32 backward on the fp32 MFMA (afa_bwd_f32.hip): head_dim 32/64/128, contiguous tensors,
+// 16-byte aligned.  e_ws holds 2 * B*H*L floats (E, then 1/d).
+bool f32_bwd_supported(int head_dim);
+hipError_t f32_bwd_launch(const GenArgs& a, hipStream_t st);
 hipError_t generic_bwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 
 hipError_t ago_tables_launch(int table_dtype, int pairs, int len, const void* freqs, double base,

@@ -53,6 +53,8 @@ WORKLOADS = {
               "C5: AFA analytical backward (dq, dk, dv), causal, head_dim 128"),
     "c3bwd": (8, 12, 4096, 64, "bf16", True, "c3", True,
               "C3: AFA analytical backward (dq, dk, dv), causal, Cayley rotary"),
+    "c4f32bwd": (32, 4, 1024, 64, "fp32", True, "default", True,
+                 "C4 (fp32): AFA analytical backward (dq, dk, dv), causal, default Cayley rotary"),
 }
 # A-Softmax over the last axis of (rows, cols) scores: name -> (rows, cols, dtype, backward, description)
 SOFTMAX_WORKLOADS = {

@@ -80,7 +80,8 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
  * as used by the pallas_afa custom VJP (:532-615).  Inputs: the forward's q, k, v, out and
  * denom (= d_total, fp32; fp64 for AFA_F64) and the output cotangent g (same layout as q).
  * Outputs dq, dk, dv (contiguous).  With rotary tables the forward rotated q and k, and the
- * returned dq, dk are with respect to the unrotated inputs; on the bf16/fp16 matrix-core path
+ * returned dq, dk are with respect to the unrotated inputs (the fp32 matrix-core kernels rotate
+ * them as tiles are staged); on the bf16/fp16 matrix-core path
  * (head_dim 32, 48, 64, 96, 128) q and k are then rotated once into
  * 2*batch*heads*seq_len*head_dim elements of stream-ordered scratch (hipMallocAsync, freed on `stream` before the call returns; if that
  * allocation fails the generic kernel runs instead).  workspace: at least

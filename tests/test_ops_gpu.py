@@ -192,6 +192,39 @@ def test_mfma_backward_with_rotary_tables(shape, causal, valid, dt):
         assert e_r <= 3e-2
 
 
+@pytest.mark.parametrize("shape,causal,valid,rot", [
+    ((1, 2, 256, 64), True, None, False), ((2, 3, 200, 64), False, None, True), ((1, 2, 300, 32), True, 257, False),
+    ((1, 1, 7, 32), True, None, True), ((1, 2, 256, 128), True, None, True), ((2, 1, 130, 128), False, 100, False),
+])
+def test_fp32_mfma_backward(shape, causal, valid, rot):
+    """The fp32 backward on the fp32 matrix cores against the generic fp32 kernel (forced with
+    AFA_FLAG_GENERIC) and the float64 oracle, with and without Cayley tables."""
+    from algebraic_intelligence_amd import _lib
+    B, H, L, D = shape
+    q, k, v = make_qkv(shape, torch.float32, seed=sum(shape) + 27)
+    g = make_qkv(shape, torch.float32, seed=sum(shape) + 28)[0]
+    rt, cf, sf = None, None, None
+    if rot:
+        c, s_ = O.cayley_tables(D, L + 2, freqs=10000.0 ** (-2.0 * np.arange(D // 2) / D))
+        c32, s32 = c.astype(np.float32), s_.astype(np.float32)
+        rt = (torch.from_numpy(c32).to(DEV), torch.from_numpy(s32).to(DEV))
+        cf, sf = c32[:L].astype(np.float64), s32[:L].astype(np.float64)
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, causal, valid, rt, 0, True)
+    mq, mk, mv = _bwd_flags(q, k, v, out, den, g, causal, valid, 0, rt)
+    gq, gk, gv = _bwd_flags(q, k, v, out, den, g, causal, valid, _lib.FLAG_GENERIC, rt)
+    qr, kr = to_f64(q), to_f64(k)
+    if rot:
+        qr, kr = O.rotate_pairs(qr, cf, sf), O.rotate_pairs(kr, cf, sf)
+    rq, rk, rv = O.afa_backward(qr, kr, to_f64(v), to_f64(g), 0.5, causal, valid)
+    if rot:
+        rq, rk = O.rotate_pairs(rq, cf, -sf), O.rotate_pairs(rk, cf, -sf)
+    for name, m, gen, r in (("dq", mq, gq, rq), ("dk", mk, gk, rk), ("dv", mv, gv, rv)):
+        assert torch.isfinite(m).all(), name
+        e_g, e_r = normwise(to_f64(m), to_f64(gen)), normwise(to_f64(m), r)
+        print(f"fp32 {shape} causal={causal} valid={valid} rot={rot} {name}: vs generic {e_g:.2e} vs fp64 {e_r:.2e}")
+        assert e_g <= 1e-5 and e_r <= 1e-5
+
+
 def test_backward_with_fused_rotation():
     """dq, dk are gradients with respect to the unrotated q, k: R^T applied to the gradients of
     the rotated inputs."""
