@@ -220,7 +220,25 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
       a.q_scale = (float)(1.0 / std::sqrt((double)head_dim));
       a.omega = (float)sink_omega;
       a.w_unscale = 1.0f;
-      return hip_status(afa::f32_fwd_launch((int)head_dim, a, s));
+      // fewer 128-query workgroups than CUs: split every query block's key tiles over up to
+      // 2 * CUs workgroups in all (partials in stream-ordered scratch, then a combine kernel)
+      const int64_t nwg = batch * heads * ((seq_len + 127) / 128);
+      const int64_t key_tiles = (vlen + 31) / 32;
+      const int64_t cus = cu_count();
+      int nsplit = 1;
+      if (nwg < cus && key_tiles > 1) nsplit = (int)std::min<int64_t>(key_tiles, (2 * cus + nwg - 1) / nwg);
+      void* part = nullptr;
+      if (nsplit > 1) {
+        part = scratch_alloc(afa::f32_fwd_part_floats(a, (int)head_dim, nsplit) * sizeof(float), s);
+        if (part == nullptr) nsplit = 1;
+      }
+      a.part = (float*)part;
+      hipError_t e = afa::f32_fwd_launch((int)head_dim, a, nsplit, s);
+      if (part != nullptr) {
+        hipError_t e2 = hipFreeAsync(part, s);
+        if (e == hipSuccess) e = e2;
+      }
+      return hip_status(e);
     }
   }
   if (head_dim > 256) return AFA_ERR_UNSUPPORTED;

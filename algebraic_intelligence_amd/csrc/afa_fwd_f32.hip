@@ -14,6 +14,9 @@
 // K/V tiles of 32 keys are staged through registers into double-buffered, padded LDS rows (the
 // Cayley rotation of k is applied in that pass, as the generic kernel does), one barrier per tile.
 // Query blocks are dispatched heaviest first (block_item).
+// Small grids (fewer workgroups than CUs) split every query block's key tiles over blockIdx.y:
+// the numerator and denominator are sums over keys, so each split writes its partial O and row
+// sum, and afa_fwd_f32_combine_kernel adds them, adds the sink and divides.
 #include "afa_common.h"
 #include "afa_launch.h"
 
@@ -38,7 +41,7 @@ __device__ __forceinline__ float rot_second(float c, float s, float x0, float x1
 
 }  // namespace
 
-template <int D, bool ROT>
+template <int D, bool ROT, bool SPLIT>
 __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
   constexpr int LDR = D + 4;   // padded LDS row: consecutive rows shift by 16 bytes (no conflicts)
   constexpr int KH = D / 2;    // head_dim entries per lane group
@@ -61,7 +64,14 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
   const int qi = q0_w + l32;
   const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 128)) : vlen;
   const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
-  const int ntiles = (kend_wg + KT - 1) / KT;
+  const int ntiles_wg = (kend_wg + KT - 1) / KT;
+  // this workgroup's key tiles [t_beg, ntiles): all of them, or one of gridDim.y even parts
+  int t_beg = 0, ntiles = ntiles_wg;
+  if constexpr (SPLIT) {
+    const int per = (ntiles_wg + (int)gridDim.y - 1) / (int)gridDim.y;
+    t_beg = min(ntiles_wg, (int)blockIdx.y * per);
+    ntiles = min(ntiles_wg, t_beg + per);
+  }
   const float* qp = (const float*)a.q + b * a.q_b + h * a.q_h;
   const float* kp = (const float*)a.k + b * a.k_b + h * a.k_h;
   const float* vp = (const float*)a.v + b * a.v_b + h * a.v_h;
@@ -142,12 +152,12 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
   float dsum = 0.f;
   const float scale = a.q_scale;
 
-  if (ntiles > 0) {
-    load(0);
-    store(0);
+  if (t_beg < ntiles) {
+    load(t_beg);
+    store(t_beg & 1);
   }
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
+  for (int t = t_beg; t < ntiles; ++t) {
     if (t + 1 < ntiles) load(t + 1);  // global loads in flight during this tile's MFMAs
     const int key0 = t * KT;
     if (key0 < kend_w && q0_w < L) {
@@ -188,6 +198,27 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
   }
 
   dsum += __shfl_xor(dsum, 32);
+  if constexpr (SPLIT) {
+    // unnormalised partials of split blockIdx.y: the numerators of all splits (each B, H, L, D),
+    // then the row sums of all splits (each B, H, L)
+    const int64_t rows = (int64_t)a.B * a.H * L;
+    float* po = a.part + (int64_t)blockIdx.y * rows * D;
+    float* pd = a.part + (int64_t)gridDim.y * rows * D + (int64_t)blockIdx.y * rows;
+    if (qi < L) {
+      float* op = po + ((int64_t)bh * L + qi) * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          f32x4_t w;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u];
+          *(f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g) = w;
+        }
+      if (g == 0) pd[(int64_t)bh * L + qi] = dsum;
+    }
+    return;
+  }
   if (qi < L) {
     const float tot = dsum + a.omega;
     float* op = (float*)a.out + b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
@@ -204,23 +235,68 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
   }
 }
 
+// out = (sum of the split numerators) / (sum of the split row sums + sink), in split order; one
+// thread per 4 features of a row.
+template <int D>
+__global__ __launch_bounds__(256) void afa_fwd_f32_combine_kernel(const FwdArgs a, int nsplit) {
+  const int64_t rows = (int64_t)a.B * a.H * a.L;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * (D / 4)) return;
+  const int64_t row = idx / (D / 4);
+  const int c4 = (int)(idx % (D / 4));
+  float tot = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < nsplit; ++sp) {
+    tot += a.part[(int64_t)nsplit * rows * D + (int64_t)sp * rows + row];
+    const f32x4_t v = *(const f32x4_t*)(a.part + (int64_t)sp * rows * D + row * D + 4 * c4);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += v[u];
+  }
+  tot += a.omega;
+  const int bh = (int)(row / a.L), l = (int)(row % a.L);
+  const int b = bh / a.H, h = bh % a.H;
+  float* op = (float*)a.out + b * a.o_b + h * a.o_h + (int64_t)l * a.o_l + 4 * c4;
+  f32x4_t w;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) w[u] = acc[u] / tot;
+  *(f32x4_t*)op = w;
+  if (a.denom != nullptr && c4 == 0) a.denom[row] = tot;
+}
+
 bool f32_fwd_supported(int head_dim) { return head_dim == 32 || head_dim == 64 || head_dim == 128; }
 
-template <int D>
-static hipError_t f32_launch_d(const FwdArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)(a.B * a.H * a.nqb));
+size_t f32_fwd_part_floats(const FwdArgs& a, int head_dim, int nsplit) {
+  return (size_t)nsplit * a.B * a.H * a.L * (head_dim + 1);
+}
+
+template <int D, bool SPLIT>
+static void f32_launch_s(const FwdArgs& a, int nsplit, hipStream_t st) {
+  const dim3 grid((unsigned)(a.B * a.H * a.nqb), (unsigned)nsplit);
   if (a.rc != nullptr)
-    hipLaunchKernelGGL((afa_fwd_f32_kernel<D, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((afa_fwd_f32_kernel<D, true, SPLIT>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((afa_fwd_f32_kernel<D, false>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((afa_fwd_f32_kernel<D, false, SPLIT>), grid, dim3(256), 0, st, a);
+}
+
+template <int D>
+static hipError_t f32_launch_d(const FwdArgs& a, int nsplit, hipStream_t st) {
+  if (nsplit <= 1) {
+    f32_launch_s<D, false>(a, 1, st);
+    return hipGetLastError();
+  }
+  if (a.part == nullptr) return hipErrorInvalidValue;
+  f32_launch_s<D, true>(a, nsplit, st);
+  const int64_t n = (int64_t)a.B * a.H * a.L * (D / 4);
+  hipLaunchKernelGGL((afa_fwd_f32_combine_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a,
+                     nsplit);
   return hipGetLastError();
 }
 
-hipError_t f32_fwd_launch(int head_dim, FwdArgs a, hipStream_t st) {
+hipError_t f32_fwd_launch(int head_dim, FwdArgs a, int nsplit, hipStream_t st) {
   a.nqb = (a.L + 127) / 128;
-  if (head_dim == 32) return f32_launch_d<32>(a, st);
-  if (head_dim == 64) return f32_launch_d<64>(a, st);
-  return f32_launch_d<128>(a, st);
+  if (head_dim == 32) return f32_launch_d<32>(a, nsplit, st);
+  if (head_dim == 64) return f32_launch_d<64>(a, nsplit, st);
+  return f32_launch_d<128>(a, nsplit, st);
 }
 
 }  // namespace afa

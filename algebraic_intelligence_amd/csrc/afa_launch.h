@@ -24,6 +24,7 @@ struct FwdArgs {
   float omega;      // sink_omega times the weight scale
   float w_unscale;  // denominator output = w_unscale * (D' + omega)
   float s_mult;     // fp32 factor of the score after the q_scale fold (kernels that take one)
+  float* part;      // split-K partials (afa_fwd_f32.hip): nsplit x B H L D numerators, then nsplit x B H L sums
 };
 
 // Generic forward / backward (afa_generic.hip).
@@ -69,7 +70,11 @@ hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
 // fp32 forward on the fp32 MFMA (afa_fwd_f32.hip): head_dim 32/64/128, V and out rows 16-byte
 // aligned; q_scale carries 1/sqrt(head_dim) (applied to the fp32 dot product).
 bool f32_fwd_supported(int head_dim);
-hipError_t f32_fwd_launch(int head_dim, FwdArgs a, hipStream_t st);
+// nsplit > 1: the key range of every query block is split over nsplit workgroups whose partial
+// numerators and row sums go to a.part (f32_fwd_part_floats(a, head_dim, nsplit) floats), then
+// a combine kernel writes out and denom.
+size_t f32_fwd_part_floats(const FwdArgs& a, int head_dim, int nsplit);
+hipError_t f32_fwd_launch(int head_dim, FwdArgs a, int nsplit, hipStream_t st);
 
 hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
 // MFMA backward (afa_bwd_mfma.hip): bf16/fp16, head_dim 64 or 128, seq_len a multiple of 4,

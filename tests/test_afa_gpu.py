@@ -301,9 +301,13 @@ def test_device_lds_limit_reported():
     ((1, 2, 130, 32), True, None, True), ((2, 1, 392, 128), False, 300, False),
     ((1, 2, 256, 128), True, None, True), ((3, 5, 129, 64), True, None, False),
 ])
-def test_fp32_mfma_vs_generic_and_fp64(shape, causal, valid, rot):
+@pytest.mark.parametrize("wide", [False, True])
+def test_fp32_mfma_vs_generic_and_fp64(shape, causal, valid, rot, wide):
     """The fp32 matrix-core kernel (afa_fwd_f32.hip) against the generic fp32 kernel
-    (AFA_FLAG_GENERIC) and the float64 oracle: the same fp32 contract in another summation order."""
+    (AFA_FLAG_GENERIC) and the float64 oracle: the same fp32 contract in another summation order.
+    Small grids split the key tiles over several workgroups and add the partials (split-K);
+    `wide` repeats the heads until the grid has a 128-query workgroup per CU, which runs unsplit,
+    and checks every copy of a head is bitwise equal."""
     B, H, L, D = shape
     q, k, v = make_qkv(shape, torch.float32, seed=sum(shape) + 3)
     rotary = None
@@ -312,11 +316,20 @@ def test_fp32_mfma_vs_generic_and_fp64(shape, causal, valid, rot):
         rotary = A.build_cayley_rotary_matrix(D, L, freqs=torch.from_numpy(_c3_freqs(D)).cuda())
         c, s = rotary.c.double().cpu().numpy(), rotary.s.double().cpu().numpy()
         qr, kr = O.rotate_pairs(qr, c, s), O.rotate_pairs(kr, c, s)
+    ref, dref = O.afa_forward(qr, kr, to_f64(v), 0.5, causal, valid, return_denominator=True)
+    reps = -(-_cu_count() // (B * H * -(-L // 128))) if wide else 1
+    if wide:
+        q, k, v = (x.repeat(1, reps, 1, 1).contiguous() for x in (q, k, v))
     a, da = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
     b, db = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_GENERIC)
-    ref, dref = O.afa_forward(qr, kr, to_f64(v), 0.5, causal, valid, return_denominator=True)
-    e_g, e_r = normwise(to_f64(a), to_f64(b)), normwise(to_f64(a), ref)
-    print(f"fp32 {shape} causal={causal} valid={valid} rot={rot}: vs generic {e_g:.2e} vs fp64 {e_r:.2e}")
+    e_g = normwise(to_f64(a), to_f64(b))
+    if wide:
+        assert torch.equal(a, a[:, :H].repeat(1, reps, 1, 1))
+        assert torch.equal(da, da[:, :H].repeat(1, reps, 1, 1))
+        a, da = a[:, :H], da[:, :H]
+    e_r = normwise(to_f64(a), ref)
+    print(f"fp32 {shape} causal={causal} valid={valid} rot={rot} wide={wide} (x{reps}): vs generic {e_g:.2e} "
+          f"vs fp64 {e_r:.2e}")
     assert e_g <= 1e-5 and e_r <= 1e-5
     assert normwise(to_f64(da), dref) <= 1e-5
 
