@@ -62,7 +62,8 @@ __device__ __forceinline__ u32x4_t bscale(u32x4_t w, float sc) {
 // Element offset of 16-byte chunk `c` of row `r` in a swizzled tile of D-element rows.
 template <int D>
 __device__ __forceinline__ int swz(int r, int c) {
-  return r * D + ((c ^ (r & 7)) << 3);
+  // (c & ~7) is a compile-time constant at every call, so chunks 8 apart share one lane offset
+  return r * D + ((((c & 7) ^ (r & 7)) | (c & ~7)) << 3);
 }
 
 // Row fragment: 8 elements (chunk c) of row r.
@@ -275,8 +276,11 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       const int lc = pc ^ (row & 7);
       unsigned short* kd = &lds_k[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* vd = &lds_v[t & 1][(256 * i + wave * 64) * 8];
-      const void* ks = (const void*)(kp + (int64_t)key * D + lc * 8);
-      const void* vs = (const void*)(vp + (int64_t)key * D + lc * 8);
+      // byte offset within the head (L * D < 2^31, mfma_bwd_supported): a uniform base plus a
+      // 32-bit lane offset
+      const uint32_t off = (uint32_t)(key * D + lc * 8) * 2u;
+      const void* ks = (const void*)((const char*)kp + off);
+      const void* vs = (const void*)((const char*)vp + off);
       if constexpr (D < DP) {
         if (lc >= D / 8) ks = vs = (const void*)afa_bwd_zero_chunk;
       }
@@ -369,11 +373,16 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
 
 // ------------------------------------------------------------------------------ dK, dV
 template <int DT, int D, bool EXACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(padded_dim(D) == 64 ? 2 : 1,
-                                                                     padded_dim(D) == 64 ? 2 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   constexpr int DP = padded_dim(D);
-  constexpr int QT = 64;
+  // At DP = 128 the V rows of the workgroup's 128 keys stay in LDS instead of registers (the
+  // k, v, dk, dv registers alone would take 192 VGPRs), with 32-row query tiles, so two waves fit
+  // per SIMD and two workgroups per CU.
+  constexpr bool VLDS = DP == 128;
+  constexpr int QT = VLDS ? 32 : 64;
+  constexpr int SUBS = QT / 32;  // 32-query sub-tiles per tile
+  constexpr int LPE = QT / 4;    // lanes loading E (and as many 1/d), 4 rows each
   constexpr int NCK = DP / 8;
   constexpr int CPT = QT * NCK / 256;
   constexpr int NKC = DP / 16;
@@ -383,6 +392,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned short lds_q[2][QT * DP];
   __shared__ __attribute__((aligned(16))) unsigned short lds_g[2][QT * DP];
   __shared__ __attribute__((aligned(16))) float lds_ei[2][2 * QT];  // E then 1/d of the tile's rows
+  __shared__ __attribute__((aligned(16))) unsigned short lds_vk[VLDS ? 128 * DP : 8];  // V rows
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -407,15 +417,30 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   const float* ep = (const float*)a.e_ws + (int64_t)bh * LP;
   const float* ip = (const float*)a.e_ws + (int64_t)BH * LP + (int64_t)bh * LP;
 
-  u32x4_t kf[NKC], vf[NKC];
+  u32x4_t kf[NKC], vf[VLDS ? 1 : NKC];
 #pragma unroll
   for (int kc = 0; kc < NKC; ++kc) {
     u32x4_t z = {0u, 0u, 0u, 0u};
     kf[kc] = z;
-    vf[kc] = z;
+    if constexpr (!VLDS) vf[kc] = z;
     if (kj < L && 16 * kc + 8 * g < D) {
       kf[kc] = bscale<DT>(*(const u32x4_t*)(kp + (int64_t)kj * D + 16 * kc + 8 * g), 0.125f);
-      vf[kc] = *(const u32x4_t*)(vp + (int64_t)kj * D + 16 * kc + 8 * g);
+      if constexpr (!VLDS) vf[kc] = *(const u32x4_t*)(vp + (int64_t)kj * D + 16 * kc + 8 * g);
+    }
+  }
+  if constexpr (VLDS) {
+    // the 128 V rows of the workgroup's keys, swizzled like the tiles (rows past L: finite data)
+#pragma unroll
+    for (int i = 0; i < 128 * NCK / 256; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / NCK, pc = c % NCK;
+      const int key = min(k0_wg + row, L - 1);
+      const int lc = pc ^ (row & 7);
+      const void* vs = (const void*)((const char*)vp + (uint32_t)(key * D + lc * 8) * 2u);
+      if constexpr (D < DP) {
+        if (lc >= D / 8) vs = (const void*)afa_bwd_zero_chunk;
+      }
+      __builtin_amdgcn_global_load_lds(vs, (void*)&lds_vk[(256 * i + wave * 64) * 8], 16, 0, 0);
     }
   }
   f32x16_t dk[NFB], dv[NFB];
@@ -436,20 +461,21 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       const int lc = pc ^ (row & 7);
       unsigned short* qd = &lds_q[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* gd = &lds_g[t & 1][(256 * i + wave * 64) * 8];
-      const void* qs = (const void*)(qp + (int64_t)qrow * D + lc * 8);
-      const void* gs = (const void*)(gp + (int64_t)qrow * D + lc * 8);
+      const uint32_t off = (uint32_t)(qrow * D + lc * 8) * 2u;
+      const void* qs = (const void*)((const char*)qp + off);
+      const void* gs = (const void*)((const char*)gp + off);
       if constexpr (D < DP) {
         if (lc >= D / 8) qs = gs = (const void*)afa_bwd_zero_chunk;
       }
       __builtin_amdgcn_global_load_lds(qs, (void*)qd, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(gs, (void*)gd, 16, 0, 0);
     }
-    if (wave == 0 && lane < 32) {
-      // 16 lanes of E, 16 of 1/d: 4 rows per lane (the head's LP rows are a whole number of
+    if (wave == 0 && lane < 2 * LPE) {
+      // LPE lanes of E, LPE of 1/d: 4 rows per lane (the head's LP rows are a whole number of
       // chunks; rows in [L, LP) hold zeros); chunks past LP re-read the last one (masked rows)
-      const int rr = t * QT + (lane & 15) * 4;
+      const int rr = t * QT + (lane % LPE) * 4;
       const int r0 = rr < LP ? rr : LP - 4;
-      const float* src = (lane < 16 ? ep : ip) + r0;
+      const float* src = (lane < LPE ? ep : ip) + r0;
       __builtin_amdgcn_global_load_lds((const void*)src, (void*)&lds_ei[t & 1][0], 16, 0, 0);
     }
   };
@@ -464,8 +490,8 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
     const unsigned short* tg = lds_g[t & 1];
     const float* tei = lds_ei[t & 1];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int m = 2 * t + sub;                      // query sub-tile
+    for (int sub = 0; sub < SUBS; ++sub) {
+      const int m = SUBS * t + sub;                   // query sub-tile
       const bool live = wave_live && m * 32 < L && (!a.causal || m * 32 + 31 >= k0_w);
       if (live) {
         const int rq = sub * 32 + l32;
@@ -478,7 +504,12 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vf[kc], P);
+        for (int kc = 0; kc < NKC; ++kc) {
+          u32x4_t vk;
+          if constexpr (VLDS) vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
+          else vk = vf[kc];
+          P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vk, P);
+        }
         float w[16], ds[16];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
@@ -559,7 +590,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
 bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len) {
   return (dtype == AFA_BF16 || dtype == AFA_F16) &&
          (head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128) &&
-         seq_len >= 1;
+         seq_len >= 1 && seq_len * head_dim < (int64_t(1) << 31);  // 32-bit in-head offsets
 }
 
 size_t mfma_bwd_rot_bytes(const GenArgs& a) { return (size_t)a.B * a.H * a.L * a.D * 2 * 2; }
