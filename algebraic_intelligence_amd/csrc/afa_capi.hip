@@ -140,7 +140,12 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   // bf16/fp16 matrix-core kernels: the fully fused one (afa_fwd_mfma.hip, head_dim 64 and 128)
   // and the pipelined ones (head_dim 32, 48, 64, 96, 128)
   const bool fused_ok = afa::mfma_fwd_supported(dtype, (int)head_dim);
-  const bool pipe_ok = afa::pipe_fwd_supported(dtype, (int)head_dim);
+  // the pipelined kernels address K and V rows by 32-bit byte offsets from the head's base
+  auto in_head_32 = [&](int64_t row_stride) {
+    return row_stride >= 0 && (seq_len - 1) * row_stride + head_dim < (int64_t(1) << 31);
+  };
+  const bool pipe_ok = afa::pipe_fwd_supported(dtype, (int)head_dim) && in_head_32(st.v[5]) &&
+                       in_head_32(st.v[8]);
   bool use_mfma = (fused_ok || pipe_ok) && !(flags & AFA_FLAG_GENERIC) && !(flags & AFA_FLAG_EXACT_REF);
   if (use_mfma) {
     // 16-byte vector loads/stores: 8-element aligned row strides and 16-byte aligned bases.

@@ -174,8 +174,10 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
       const int s = tid + 256 * i, r = s / CH, pc = s % CH;
       const int key = min(t * KT + r, L - 1);  // rows past L: finite data, masked
       const int lk = pc ^ (r & 7), lv = v_swizzle<DP>(r, pc);
-      const void* ks = (const void*)(kp + (int64_t)key * a.k_l + lk * 8);
-      const void* vs = (const void*)(vp + (int64_t)key * a.v_l + lv * 8);
+      // byte offsets within the head fit 32 bits (checked by the caller): a uniform base plus a
+      // 32-bit lane offset per load
+      const void* ks = (const void*)((const char*)kp + (uint32_t)(key * (int)a.k_l + lk * 8) * 2u);
+      const void* vs = (const void*)((const char*)vp + (uint32_t)(key * (int)a.v_l + lv * 8) * 2u);
       if constexpr (CHD < CH) {
         if (lk >= CHD) ks = (const void*)afa_pipe_zero_chunk;
         if (lv >= CHD) vs = (const void*)afa_pipe_zero_chunk;
