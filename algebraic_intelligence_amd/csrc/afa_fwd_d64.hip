@@ -179,27 +179,32 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   const int row0 = tid >> 3, c8 = tid & 7;     // chunk 1 is row0 + 32 (same low row bits)
   const int lcv = c8 ^ (((row0 >> 1) & 1) << 2);
   const int lck = c8 ^ (row0 & 7);
-  const unsigned short* vsrc = vp + (int64_t)row0 * a.v_l + lcv * 8;
-  const unsigned short* ksrc = kp + (int64_t)row0 * a.k_l + lck * 8;
-  const int64_t v32 = 32 * a.v_l, k32 = 32 * a.k_l;
+  // Each load is a uniform base (the tile's first row) plus a 32-bit lane offset: the caller
+  // routes only strides whose in-head byte offsets fit 32 bits here.
+  const uint32_t voff = (uint32_t)(row0 * (int)a.v_l + lcv * 8) * 2u;
+  const uint32_t koff = (uint32_t)(row0 * (int)a.k_l + lck * 8) * 2u;
+  const int64_t v32 = 64 * a.v_l, k32 = 64 * a.k_l;  // bytes of 32 rows
   auto issue_tile = [&](int t) {
     unsigned short* vdst = &lds_v[t & (NB - 1)][wave * 512];
     unsigned short* kdst = &lds_k[t & (NB - 1)][wave * 512];
     if (t * KT + KT <= L) {
-      const int64_t vo = (int64_t)t * KT * a.v_l, ko = (int64_t)t * KT * a.k_l;
-      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo), (void*)vdst, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vsrc + vo + v32), (void*)(vdst + 2048), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko), (void*)kdst, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(ksrc + ko + k32), (void*)(kdst + 2048), 16, 0, 0);
+      const char* vb = (const char*)vp + (int64_t)t * KT * a.v_l * 2;
+      const char* kb = (const char*)kp + (int64_t)t * KT * a.k_l * 2;
+      __builtin_amdgcn_global_load_lds((const void*)(vb + voff), (void*)vdst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vb + v32 + voff), (void*)(vdst + 2048), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(kb + koff), (void*)kdst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(kb + k32 + koff), (void*)(kdst + 2048), 16, 0, 0);
     } else {
       // last, partial tile: rows past L read row L-1 (masked keys; the data only has to be finite)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int key = min(t * KT + row0 + 32 * i, L - 1);
-        __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)key * a.v_l + lcv * 8),
-                                         (void*)(vdst + 2048 * i), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)key * a.k_l + lck * 8),
-                                         (void*)(kdst + 2048 * i), 16, 0, 0);
+        const uint32_t vo = (uint32_t)(key * (int)a.v_l + lcv * 8) * 2u;
+        const uint32_t ko = (uint32_t)(key * (int)a.k_l + lck * 8) * 2u;
+        __builtin_amdgcn_global_load_lds((const void*)((const char*)vp + vo), (void*)(vdst + 2048 * i),
+                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)((const char*)kp + ko), (void*)(kdst + 2048 * i),
+                                         16, 0, 0);
       }
     }
   };
