@@ -373,14 +373,15 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
 
 // ------------------------------------------------------------------------------ dK, dV
 template <int DT, int D, bool EXACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(padded_dim(D) == 64 ? 3 : 2,
+                                                                     padded_dim(D) == 64 ? 3 : 2)))
 void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   constexpr int DP = padded_dim(D);
-  // At DP = 128 the V rows of the workgroup's 128 keys stay in LDS instead of registers (the
-  // k, v, dk, dv registers alone would take 192 VGPRs), with 32-row query tiles, so two waves fit
-  // per SIMD and two workgroups per CU.
-  constexpr bool VLDS = DP == 128;
-  constexpr int QT = VLDS ? 32 : 64;
+  // The V rows of the workgroup's 128 keys stay in LDS instead of registers.  At DP = 128 (where
+  // the k, v, dk, dv registers alone would take 192 VGPRs) the query tiles have 32 rows, so two
+  // waves fit per SIMD and two workgroups per CU; at DP = 64, three of each.
+  constexpr bool VLDS = true;
+  constexpr int QT = DP == 128 ? 32 : 64;
   constexpr int SUBS = QT / 32;  // 32-query sub-tiles per tile
   constexpr int LPE = QT / 4;    // lanes loading E (and as many 1/d), 4 rows each
   constexpr int NCK = DP / 8;
