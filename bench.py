@@ -361,14 +361,22 @@ def main():
                 _lib.check(r, "afa_bwd")
 
     warm = warm_up(step, args)
+    # the timed region: K calls between two events, nothing else on the stream
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    # per-call spread from a second, untimed pass with an event after every call
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     ev[0].record(stream)
     for i in range(args.steps):
         step()
         ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    ms_total = ev[0].elapsed_time(ev[-1])
-    ms = ms_total / args.steps
     ms_median = float(np.median([ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]))
     flops = A.afa_flops(B, H, L, D, causal=causal) // 4 * (10 if backward else 4)
     tflops = flops / (ms * 1e-3) / 1e12
