@@ -197,20 +197,40 @@ __global__ __launch_bounds__(256) void oace_convert_kernel(const A* x, int64_t r
 
 // y (cols x rows, leading dimension ldy) = x^T for a rows x cols matrix x of 2-byte elements
 // (leading dimension ldx, rows of any alignment), rows a multiple of 8 and y 16-byte aligned with
-// ldy a multiple of 8.  A lane gathers 8 consecutive rows of one column (each load coalesced
-// across the wave's consecutive columns) and writes them as one 16-byte segment of y.
+// ldy a multiple of 8.  A workgroup stages a 64-row x 128-column tile in LDS: each wave reads 16
+// rows, one 2-byte element per lane and column (coalesced along the row); then every 8 lanes
+// write 64 consecutive elements of one row of y (one 128-byte line), 16 bytes per lane.
+constexpr int TR_ROWS = 64, TR_COLS = 128, TR_PITCH = TR_COLS + 2;
 __global__ __launch_bounds__(256) void oace_transpose16_kernel(const unsigned short* x, int64_t rows, int64_t cols,
                                                                int64_t ldx, unsigned short* y, int64_t ldy) {
-  const int64_t c = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
-  if (c >= cols) return;
-  for (int64_t r0 = ((int64_t)blockIdx.y * 4 + (threadIdx.x >> 6)) * 8; r0 < rows; r0 += (int64_t)gridDim.y * 32) {
-    unsigned v[8];
+  __shared__ unsigned short t[TR_ROWS * TR_PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * TR_COLS, r0 = (int64_t)blockIdx.y * TR_ROWS;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = x[(r0 + j) * ldx + c];
-    u32x4_t w;
+  for (int h = 0; h < 2; ++h) {
+    const int64_t c = c0 + h * 64 + lane;
+    unsigned short v[16];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) w[e] = v[2 * e] | (v[2 * e + 1] << 16);
-    *(u32x4_t*)(y + c * ldy + r0) = w;
+    for (int i = 0; i < 16; ++i) {
+      const int64_t r = r0 + wave * 16 + i;
+      v[i] = c < cols && r < rows ? x[r * ldx + c] : (unsigned short)0;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[(wave * 16 + i) * TR_PITCH + h * 64 + lane] = v[i];
+  }
+  __syncthreads();
+  const int sg = tid & 7;  // 8-row segment of the tile
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int cl = (tid >> 3) + 32 * k;  // tile column = row of y
+    const int64_t c = c0 + cl;
+    if (c < cols && r0 + 8 * sg < rows) {
+      u32x4_t w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = (unsigned)t[(8 * sg + 2 * e) * TR_PITCH + cl] | ((unsigned)t[(8 * sg + 2 * e + 1) * TR_PITCH + cl] << 16);
+      *(u32x4_t*)(y + c * ldy + r0 + 8 * sg) = w;
+    }
   }
 }
 
@@ -397,7 +417,7 @@ hipError_t oace_softmax_bwd_launch(int dtype, const OaceArgs& a, const void* row
 hipError_t oace_transpose16(const void* x, int64_t rows, int64_t cols, int64_t ldx, void* y, int64_t ldy,
                             hipStream_t st) {
   if (rows % 8 != 0 || ldy % 8 != 0 || ((uintptr_t)y & 15u) != 0) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)std::min<int64_t>((rows + 31) / 32, 8));
+  const dim3 grid((unsigned)((cols + TR_COLS - 1) / TR_COLS), (unsigned)((rows + TR_ROWS - 1) / TR_ROWS));
   hipLaunchKernelGGL(oace_transpose16_kernel, grid, dim3(256), 0, st, (const unsigned short*)x, rows, cols, ldx,
                      (unsigned short*)y, ldy);
   return hipGetLastError();
