@@ -450,10 +450,10 @@ size_t oace_ws_size(int dtype, const afa::OaceArgs& a) {
 extern "C" {
 
 size_t oace_workspace_size(int dtype, int64_t rows, int64_t d_model, int64_t vocab, int w_layout, unsigned flags) {
-  (void)flags;
   if (!valid_dtype(dtype) || rows <= 0 || d_model <= 0 || vocab <= 0) return 0;
-  const afa::OaceArgs a = oace_args(rows, d_model, vocab, nullptr, d_model, nullptr, w_layout,
-                                    w_layout == OACE_W_DV ? vocab : d_model, nullptr, 0.0, 1.0);
+  afa::OaceArgs a = oace_args(rows, d_model, vocab, nullptr, d_model, nullptr, w_layout,
+                              w_layout == OACE_W_DV ? vocab : d_model, nullptr, 0.0, 1.0);
+  a.flags = flags & OACE_FLAG_RECOMPUTE_Z;
   return oace_ws_size(dtype, a);
 }
 
@@ -502,7 +502,7 @@ int oace_linear_bwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, con
   a.g_loss = g_loss;
   a.dh = dh;
   a.dw = dw;
-  a.flags = workspace != nullptr ? flags : flags & ~OACE_FLAG_WT_READY;
+  a.flags = workspace != nullptr ? flags : flags & ~(OACE_FLAG_WT_READY | OACE_FLAG_Z_READY);
   const size_t need = oace_ws_size(dtype, a);
   void* ws = workspace;
   bool owned = false;

@@ -43,7 +43,7 @@ constexpr int STAGE = A_BYTES + B_BYTES;
 constexpr int A_LOADS = A_BYTES / (256 * 16);  // 16-byte direct loads per thread and step
 constexpr int B_LOADS = B_BYTES / (256 * 16);
 constexpr int LOADS = A_LOADS + B_LOADS;
-constexpr int MODE_SQ = 0, MODE_OCTIC = 1, MODE_DZ = 2;
+constexpr int MODE_SQ = 0, MODE_OCTIC = 1, MODE_DZ = 2, MODE_SQZ = 3;
 
 struct GemmArgs {
   const unsigned short* wt;  // (V, d), row stride ldwt
@@ -56,6 +56,7 @@ struct GemmArgs {
   float* part;  // MODE_SQ: [nvt][N]; MODE_OCTIC: [nvt][N][4]
   unsigned short* dz;  // MODE_DZ: (N, ldz)
   int64_t ldz;
+  float* zc;  // MODE_SQZ: the fp32 logits, (N, ldz)
   float c0;
   const float* g_loss;
 };
@@ -160,7 +161,30 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
   const int vw = v0 + wave * 64;
   const bool vtail = v0 + TV > a.V;
   float* red = (float*)lds;  // the ring is idle after the last barrier
-  if constexpr (MODE == MODE_SQ) {
+  if constexpr (MODE == MODE_SQZ) {
+    // the logits themselves, 4 consecutive vocabulary entries per store (a group that starts
+    // below V ends below the padded row length; its entries past V are finite and never read)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int n = n0 + nb * 32 + l32;
+      if (n < a.N) {
+        float* zrow = a.zc + (int64_t)n * a.ldz;
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const int vs = vw + 32 * vb + 8 * e4 + 4 * g;
+            if (vs < a.V) {
+              f32x4_t w;
+#pragma unroll
+              for (int u = 0; u < 4; ++u) w[u] = acc[vb][nb][4 * e4 + u];
+              *(f32x4_t*)(zrow + vs) = w;
+            }
+          }
+      }
+    }
+  }
+  if constexpr (MODE == MODE_SQ || MODE == MODE_SQZ) {
     float s[4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
@@ -282,6 +306,84 @@ __global__ __launch_bounds__(256) void oace_mfma_tau_kernel(const float* part, i
   if (lane == 0) rows[(int64_t)n * OACE_ROW + OACE_TAU] = o_rsq<float>(ss * inv_v + eps);
 }
 
+// The octic partial sums of the cached logits (the MODE_OCTIC epilogue's quantities): one wave
+// per (row, group of ZG vocabulary entries), 16 entries per lane read as f32x4, then one
+// reduction across the wave; partials [group][N][4] in the MODE_OCTIC layout.
+constexpr int ZG = 1024;
+__global__ __launch_bounds__(256) void oace_mfma_octic_cached_kernel(const float* zc, int64_t ldz, int N, int V,
+                                                                     int ngroups, const float* rows, float* part) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)N * ngroups) return;
+  const int n = (int)(w / ngroups), grp = (int)(w % ngroups);
+  const float tau = rows[(int64_t)n * OACE_ROW + OACE_TAU];
+  const float* zrow = zc + (int64_t)n * ldz;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int it = 0; it < ZG / 256; ++it) {
+    const int v0 = grp * ZG + it * 256 + 4 * lane;
+    if (v0 < V) {
+      const f32x4_t z4 = *(const f32x4_t*)(zrow + v0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (v0 + u < V) {
+          const float x = z4[u] * tau;
+          const Oct<float> o = octic_fast(x);
+          const float rn = o.r * x;
+          s[0] += o.k8;
+          s[1] += o.rho7;
+          s[2] += rn * o.k8;
+          s[3] += rn * o.rho7;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s[q] += __shfl_xor(s[q], m);
+  if (lane == 0) {
+    float* dst = part + ((int64_t)grp * N + n) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = s[q];
+  }
+}
+
+// dz from the cached logits, 4 vocabulary entries per thread: the MODE_DZ epilogue's arithmetic
+// on the same fp32 logits; entries in [V, ldz) are written as zeros.
+template <int DT>
+__global__ __launch_bounds__(256) void oace_mfma_dz_cached_kernel(const float* zc, int64_t ldz, int N, int V,
+                                                                  const float* rows, const int64_t* targets, float c0,
+                                                                  const float* g_loss, unsigned short* dz) {
+  const int64_t q4 = ldz / 4;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)N * q4) return;
+  const int n = (int)(i / q4);
+  const int vs = (int)(i % q4) * 4;
+  const float gl = g_loss ? *g_loss : 1.f;
+  const float* rec = rows + (int64_t)n * OACE_ROW;
+  const float tau = rec[OACE_TAU], inv_S = rec[OACE_INV_S], pc = rec[OACE_PC_INV8], radial = rec[OACE_RADIAL];
+  const float scale = rec[OACE_S8] * inv_S;
+  const float diff = rec[OACE_SUM_P78] - pc;
+  const float tc = tau * (c0 * gl);
+  const int64_t t = targets[n];
+  float dzv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (vs < V) {
+    const f32x4_t z4 = *(const f32x4_t*)(zc + (int64_t)n * ldz + vs);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float x = z4[u] * tau;
+      const Oct<float> o = octic_fast(x);
+      const float bracket = scale * o.rho7 - (vs + u == t ? pc : 0.f) - (o.k8 * inv_S) * diff;
+      dzv[u] = vs + u < V ? tc * (o.r * bracket - radial * x) : 0.f;
+    }
+  }
+  u32x2_t w;
+  w[0] = Elem<DT>::pack(dzv[0], dzv[1]);
+  w[1] = Elem<DT>::pack(dzv[2], dzv[3]);
+  *(u32x2_t*)(dz + (int64_t)n * ldz + vs) = w;
+}
+
 // Row records from the MODE_OCTIC partials, one wave per row.  The target logit is the dot
 // product of the row of h with row t of W^T (fp32 accumulation of the exact element products,
 // as the GEMM); a target outside [0, V) leaves rho_t = 0 (infinite loss), as the reference.
@@ -352,18 +454,28 @@ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int dh_splits(const OaceArgs& a);
 
+// The forward keeps the fp32 logits (rows x padded vocabulary) when they take at most this many
+// bytes -- the reference benchmark's 512 x 50257 take 103 MB, which the 256 MB Infinity Cache
+// holds -- and then evaluates the octic sums, and the backward dz, from them instead of a
+// second GEMM sweep.  Larger problems recompute z, which keeps the workspace O(rows x d_model).
+constexpr size_t ZC_MAX_BYTES = (size_t)256 << 20;
+bool z_cached(const OaceArgs& a) {
+  return !(a.flags & OACE_FLAG_RECOMPUTE_Z) && (size_t)a.N * ldz_of(a.V) * sizeof(float) <= ZC_MAX_BYTES;
+}
+
 struct Layout {
-  size_t wt, part, dz, dhp, blas, total;
+  size_t wt, zc, part, dz, dhp, blas, total;
 };
 Layout layout_of(const OaceArgs& a) {
   Layout l;
   l.wt = a.w_layout == OACE_W_DV ? al((size_t)a.V * a.d * 2) : 0;
+  l.zc = z_cached(a) ? al((size_t)a.N * ldz_of(a.V) * sizeof(float)) : 0;
   l.part = al((size_t)nvt_of(a.V) * a.N * 4 * sizeof(float));
   l.dz = al((size_t)a.N * ldz_of(a.V) * 2);
   const int s = dh_splits(a);
   l.dhp = s > 1 ? al((size_t)(s + 1) * a.d * a.N * sizeof(float)) : 0;  // split-K partials of dh
   l.blas = BLAS_WS;
-  l.total = l.wt + std::max(l.part, l.dz + l.dhp + l.blas);
+  l.total = l.wt + l.zc + std::max(l.part, l.dz + l.dhp + l.blas);
   return l;
 }
 
@@ -598,23 +710,41 @@ hipError_t oace_linear_fwd_mfma(int dtype, const OaceArgs& a, void* rows, void* 
   int64_t ldwt = 0;
   const unsigned short* wt = wt_of(a, base, ldwt, st, e);
   if (e != hipSuccess) return e;
-  float* part = (float*)(base + l.wt);
+  float* part = (float*)(base + l.wt + l.zc);
   GemmArgs g = gemm_args(a, wt, ldwt);
   g.rows = (const float*)rows;
   g.part = part;
   const float inv_v = (float)(1.0 / (double)a.V);
-  if ((e = launch_gemm_dt<MODE_SQ>(dtype, g, st)) != hipSuccess) return e;
+  const bool zc = l.zc > 0;
+  if (zc) {
+    g.zc = (float*)(base + l.wt);
+    g.ldz = ldz_of(a.V);
+    e = launch_gemm_dt<MODE_SQZ>(dtype, g, st);
+  } else {
+    e = launch_gemm_dt<MODE_SQ>(dtype, g, st);
+  }
+  if (e != hipSuccess) return e;
   const unsigned rg = (unsigned)((a.N + 3) / 4);
   hipLaunchKernelGGL(oace_mfma_tau_kernel, dim3(rg), dim3(256), 0, st, (const float*)part, g.nvt, g.N, inv_v,
                      (float)a.eps, (float*)rows);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  if ((e = launch_gemm_dt<MODE_OCTIC>(dtype, g, st)) != hipSuccess) return e;
+  int nparts = g.nvt;  // partial sums per row for the row kernel
+  if (zc) {
+    nparts = (int)((a.V + ZG - 1) / ZG);
+    const unsigned og = (unsigned)(((int64_t)a.N * nparts + 3) / 4);
+    hipLaunchKernelGGL(oace_mfma_octic_cached_kernel, dim3(og), dim3(256), 0, st, (const float*)g.zc, g.ldz, g.N,
+                       g.V, nparts, (const float*)rows, part);
+    e = hipGetLastError();
+  } else {
+    e = launch_gemm_dt<MODE_OCTIC>(dtype, g, st);
+  }
+  if (e != hipSuccess) return e;
   const unsigned wg = (unsigned)((a.N + 3) / 4);
   if (dtype == AFA_BF16)
-    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_BF16>, dim3(wg), dim3(256), 0, st, (const float*)part, g.nvt, g.N,
+    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_BF16>, dim3(wg), dim3(256), 0, st, (const float*)part, nparts, g.N,
                        inv_v, (float)a.gamma, g.h, g.ldh, wt, ldwt, g.d, g.V, a.targets, (float*)rows);
   else
-    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_F16>, dim3(wg), dim3(256), 0, st, (const float*)part, g.nvt, g.N,
+    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_F16>, dim3(wg), dim3(256), 0, st, (const float*)part, nparts, g.N,
                        inv_v, (float)a.gamma, g.h, g.ldh, wt, ldwt, g.d, g.V, a.targets, (float*)rows);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return oace_mean_launch(dtype, rows, a.N, a.loss, st);
@@ -627,15 +757,30 @@ hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, 
   int64_t ldwt = 0;
   const unsigned short* wt = wt_of(a, base, ldwt, st, e);
   if (e != hipSuccess) return e;
-  unsigned short* dz = (unsigned short*)(base + l.wt);
-  void* bws = base + l.wt + l.dz;
+  char* sbase = base + l.wt + l.zc;  // the region after the cached logits
+  unsigned short* dz = (unsigned short*)sbase;
+  void* bws = sbase + l.dz;
   GemmArgs g = gemm_args(a, wt, ldwt);
   g.rows = (const float*)rows;
   g.dz = dz;
   g.ldz = ldz_of(a.V);
   g.c0 = (float)(8.0 * a.gamma / (double)a.N);
   g.g_loss = (const float*)a.g_loss;
-  if ((e = launch_gemm_dt<MODE_DZ>(dtype, g, st)) != hipSuccess) return e;
+  if (l.zc > 0 && (a.flags & OACE_FLAG_Z_READY)) {
+    // the forward's logits are in the workspace: dz elementwise
+    const float* zcp = (const float*)(base + l.wt);
+    const unsigned dg = (unsigned)(((int64_t)a.N * (g.ldz / 4) + 255) / 256);
+    if (dtype == AFA_BF16)
+      hipLaunchKernelGGL(oace_mfma_dz_cached_kernel<AFA_BF16>, dim3(dg), dim3(256), 0, st, zcp, g.ldz, g.N, g.V,
+                         (const float*)rows, a.targets, g.c0, g.g_loss, dz);
+    else
+      hipLaunchKernelGGL(oace_mfma_dz_cached_kernel<AFA_F16>, dim3(dg), dim3(256), 0, st, zcp, g.ldz, g.N, g.V,
+                         (const float*)rows, a.targets, g.c0, g.g_loss, dz);
+    e = hipGetLastError();
+  } else {
+    e = launch_gemm_dt<MODE_DZ>(dtype, g, st);
+  }
+  if (e != hipSuccess) return e;
   // dh (N, d) row-major = dz (N, V) W^T: column-major dh^T (d x N) = Wt^T-view (d x V) . dz^T-view (V x N).
   // The contraction is the whole vocabulary and the output small, so it is split into S slices of
   // the vocabulary (a strided batch into fp32 partials, plus the remainder) and reduced in order.
@@ -645,8 +790,8 @@ hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, 
                        l.blas, st)) != hipSuccess)
       return e;
   } else {
-    float* dhp = (float*)(base + l.wt + l.dz);
-    bws = base + l.wt + l.dz + l.dhp;
+    float* dhp = (float*)(sbase + l.dz);
+    bws = sbase + l.dz + l.dhp;
     const int64_t vs = a.V / S, rem = a.V - vs * S, dn = a.d * a.N;
     if ((e = blas_gemm(dtype, {false, false, a.d, a.N, vs, wt, ldwt, vs * ldwt, dz, g.ldz, vs, dhp, a.d, dn, true, S},
                        bws, l.blas, st)) != hipSuccess)

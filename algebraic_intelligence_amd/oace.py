@@ -3,8 +3,10 @@ fused_oace_softmax_loss (src/model.py:180-240), tasmaikeni13/algebraic-intellige
 
 fused_linear_oace(h, w_vocab, targets, eps_vocab=100.0, gamma=2.0, chunk_size=4096) is the mean
 octic algebraic cross-entropy of the AVN-normalised A-Softmax of z = h @ w_vocab, differentiable
-with the reference's analytical backward; the logits (rows, vocab) are never materialised on the
-bf16/fp16 path.  Every computation runs in the gfx950 kernels of libafa_hip.so (include/afa.h).
+with the reference's analytical backward.  On the bf16/fp16 path the logits (rows, vocab) are
+materialised only when they fit 256 MB (fp32, in the call's workspace, reused by the backward);
+larger problems recompute them.  Every computation runs in the gfx950 kernels of libafa_hip.so
+(include/afa.h).
 """
 from __future__ import annotations
 
@@ -20,6 +22,8 @@ __all__ = ["fused_linear_oace", "fused_linear_oace_forward", "fused_linear_oace_
 OACE_W_DV, OACE_W_VD = 0, 1
 ROW_FIELDS = 8
 FLAG_WT_READY = 0x10
+FLAG_Z_READY = 0x20
+FLAG_RECOMPUTE_Z = 0x40
 
 
 def _check_scalars(chunk_size=None, gamma=None):
@@ -80,14 +84,15 @@ def fused_linear_oace_forward(h, w_vocab, targets, eps_vocab: float = 100.0, gam
                                         t.data_ptr(), float(eps_vocab), float(gamma), loss.data_ptr(), rows.data_ptr(),
                                         flags, ws.data_ptr(), wsb, _lib.stream_ptr(dev))
     _lib.check(rc, "oace_linear_fwd")
-    cache = (hf, w_vocab, t, rows, float(gamma), chunk_size, tuple(h.shape), flags, ws, w_vocab._version)
+    cache = (hf, w_vocab, t, rows, float(gamma), chunk_size, tuple(h.shape), flags, ws, w_vocab._version,
+             hf._version)
     return loss, cache
 
 
 def fused_linear_oace_backward(cache, g):
     """(dh, dw_vocab, None) from the forward cache and the loss cotangent g
     (src/kernels/pallas_oace.py:212-269)."""
-    hf, w_vocab, t, rows, gamma, _chunk, shape, flags, ws, w_version = cache
+    hf, w_vocab, t, rows, gamma, _chunk, shape, flags, ws, w_version, h_version = cache
     dev = hf.device
     d, V = w_vocab.shape
     wop, layout, ldw = _w_operand(w_vocab)
@@ -100,8 +105,10 @@ def fused_linear_oace_backward(cache, g):
     else:
         dw_store = torch.empty((V, ldw), dtype=w_vocab.dtype, device=dev)
         dw = dw_store[:, :d].t()
-    # the forward's transposed weights are still valid unless w_vocab was modified in place since
-    bflags = flags | (FLAG_WT_READY if w_vocab._version == w_version else 0)
+    # the forward's transposed weights are still valid unless w_vocab was modified in place since,
+    # and its logits unless h or w_vocab was
+    w_same = w_vocab._version == w_version
+    bflags = flags | (FLAG_WT_READY if w_same else 0) | (FLAG_Z_READY if w_same and hf._version == h_version else 0)
     with torch.cuda.device(dev):
         rc = _lib.lib().oace_linear_bwd(_lib.dtype_code(hf.dtype), hf.shape[0], d, V, hf.data_ptr(), hf.stride(0),
                                         wop.data_ptr(), layout, ldw, t.data_ptr(), float(gamma), rows.data_ptr(),

@@ -250,9 +250,10 @@ def oace_bench(args, dev):
             _lib.check(r, "oace_linear_fwd")
 
     def bwd():
-        # same workspace as the forward: its transposed weights are reused (OACE_FLAG_WT_READY)
+        # same workspace as the forward, h and w unchanged: its transposed weights and (when it kept
+        # them) its logits are reused (OACE_FLAG_WT_READY | OACE_FLAG_Z_READY)
         r = lib.oace_linear_bwd(_lib.AFA_BF16, N, d, V, h.data_ptr(), d, w.data_ptr(), 0, V, t.data_ptr(), 2.0,
-                                rows.data_ptr(), one.data_ptr(), dh.data_ptr(), dw.data_ptr(), 0x10, ws.data_ptr(),
+                                rows.data_ptr(), one.data_ptr(), dh.data_ptr(), dw.data_ptr(), 0x30, ws.data_ptr(),
                                 wsb, stream.cuda_stream)
         if r != 0:
             _lib.check(r, "oace_linear_bwd")
@@ -272,8 +273,12 @@ def oace_bench(args, dev):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     nvd = 2 * N * V * d
-    fwd_flops = nvd + min(nvd, 2 * d * d * V + 2 * N * d * d)
-    flops = {False: fwd_flops, True: 3 * nvd, "step": fwd_flops + 3 * nvd}[backward]
+    # the logits once; their second moment from a second sweep (or the Gram route) unless the forward
+    # keeps them (fp32 rows x padded vocabulary within 256 MB), when the backward reuses them too
+    z_kept = N * (-(-V // 64) * 64) * 4 <= 256 << 20
+    fwd_flops = nvd if z_kept else nvd + min(nvd, 2 * d * d * V + 2 * N * d * d)
+    bwd_flops = 2 * nvd if z_kept else 3 * nvd
+    flops = {False: fwd_flops, True: bwd_flops, "step": fwd_flops + bwd_flops}[backward]
     tflops = flops / (ms * 1e-3) / 1e12
     if not torch.isfinite(loss):
         raise RuntimeError("non-finite loss")
@@ -286,7 +291,7 @@ def oace_bench(args, dev):
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: h, W ~ N(0,1) bf16, uniform targets, resident in HBM",
         "config": {"workload": workload, "rows": N, "d_model": d, "vocab": V, "w_layout": "(d_model, vocab)",
-                   "flops_per_step": flops},
+                   "logits_kept": z_kept, "flops_per_step": flops},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
     }), flush=True)

@@ -161,6 +161,14 @@ int ago_rotate(int dtype, int64_t outer, int64_t seq_len, int64_t inner, int64_t
    and the weights have not changed since; the transposed copy of an OACE_W_DV weight that call
    left in it is reused. */
 #define OACE_FLAG_WT_READY 0x10u
+/* oace_linear_bwd: as OACE_FLAG_WT_READY, and h has not changed either; the fp32 logits that the
+   forward keeps in the workspace (bf16/fp16 when rows x vocab x 4 bytes fit 256 MB) are reused,
+   so dz is formed elementwise instead of by a second GEMM.  No counterpart in the reference. */
+#define OACE_FLAG_Z_READY 0x20u
+/* oace_workspace_size / oace_linear_fwd / oace_linear_bwd (the same on all three): never keep
+   the logits; the backward recomputes them (a workspace of O(rows x d_model + vocab x d_model)).
+   No counterpart in the reference. */
+#define OACE_FLAG_RECOMPUTE_Z 0x40u
 size_t oace_workspace_size(int dtype, int64_t rows, int64_t d_model, int64_t vocab, int w_layout,
                            unsigned flags);
 int oace_linear_fwd(int dtype, int64_t rows, int64_t d_model, int64_t vocab, const void* h,

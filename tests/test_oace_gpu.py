@@ -130,9 +130,10 @@ def test_linear_generic_vs_oracle(shape, dtype, tied):
 @pytest.mark.parametrize("shape", [(8, 64, 300), (130, 96, 1000), (512, 768, 50257), (3, 32, 7)])
 @pytest.mark.parametrize("tied", [False, True])
 def test_linear_mfma_vs_oracle_and_generic(shape, dtype, tied):
-    """The MFMA path (two GEMM sweeps with fused epilogues, dz GEMM + hipBLASLt) against the
-    float64 oracle on the same exact inputs and against the generic kernels (AFA_FLAG_GENERIC);
-    (512, 768, 50257) is the reference benchmark's configuration (scripts/benchmark_kernels.py:118)."""
+    """The MFMA path (one GEMM sweep keeping the fp32 logits, the octic sums and dz from them,
+    hipBLASLt for dh and dW) against the float64 oracle on the same exact inputs and against the
+    generic kernels (AFA_FLAG_GENERIC); (512, 768, 50257) is the reference benchmark's
+    configuration (scripts/benchmark_kernels.py:118)."""
     N, d, V = shape
     h, w, t = _case(N, d, V, dtype, seed=N + d + V, scale=1.0 if dtype == torch.bfloat16 else 0.5)
     if tied:
@@ -154,6 +155,43 @@ def test_linear_mfma_vs_oracle_and_generic(shape, dtype, tied):
     assert abs(float(loss) - float(gl)) <= 2e-5 * abs(float(gl))
     assert e_h <= 2e-2 and e_w <= 2e-2
     assert e_gh <= 2e-2 and e_gw <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", LOW)
+@pytest.mark.parametrize("shape", [(130, 96, 1000), (512, 768, 50257), (3, 32, 7)])
+@pytest.mark.parametrize("tied", [False, True])
+def test_kept_logits_match_recomputed(shape, dtype, tied):
+    """The forward that keeps the fp32 logits (octic sums from them) against the two-sweep forward
+    (OACE_FLAG_RECOMPUTE_Z): the same sums in another order.  On one forward's row records, the
+    backward's dz from the kept logits (OACE_FLAG_Z_READY) against the dz GEMM sweep: the same
+    fp32 logits and arithmetic, so dh and dW are bitwise equal."""
+    N, d, V = shape
+    h, w, t = _case(N, d, V, dtype, seed=N + 2 * d + V, scale=1.0 if dtype == torch.bfloat16 else 0.5)
+    if tied:
+        w = _tied(w)
+    loss, cache = _fwd(h, w, t)
+    rloss, rcache = _fwd(h, w, t, flags=A.oace.FLAG_RECOMPUTE_Z)
+    assert abs(float(loss) - float(rloss)) <= 1e-6 * abs(float(rloss))
+    assert normwise(to_f64(cache[3][:, :7]), to_f64(rcache[3][:, :7])) <= 1e-6
+    dh, dw = _grads(cache, 1.0)
+    stale_h = cache[:-1] + (-1,)  # as if h had changed: the backward recomputes z by the GEMM sweep
+    gh, gw = _grads(stale_h, 1.0)
+    assert torch.equal(dh, gh) and torch.equal(dw, gw)
+    rh, rw = _grads(rcache, 1.0)
+    assert normwise(to_f64(dh), to_f64(rh)) <= 1e-3 and normwise(to_f64(dw), to_f64(rw)) <= 1e-3
+
+
+def test_backward_after_inputs_change_in_place():
+    """The forward's kept logits are reused only while h and w_vocab are unchanged; after an
+    in-place update of h the backward recomputes them with the current h."""
+    h, w, t = _case(16, 64, 700, torch.bfloat16, seed=23)
+    loss, cache = _fwd(h, w, t)
+    h.mul_(0.5)
+    dh, dw = _grads(cache, 1.0)
+    hf, wf, tn = to_f64(h), to_f64(w), t.cpu().numpy()
+    rows = {k: to_f64(cache[3][:, i:i + 1]) for i, k in enumerate(O.ROW_FIELDS)}
+    rh, rw = O.fused_linear_oace_backward(hf, wf, tn, rows, g=1.0)
+    assert normwise(to_f64(dh), rh) <= 2e-2 and normwise(to_f64(dw), rw) <= 2e-2
 
 
 def test_linear_autograd_and_chunk_size():
