@@ -288,71 +288,97 @@ __global__ __launch_bounds__(256) void asoftmax_bwd_reg_kernel(int64_t rows, int
                                                                const void* g, void* dx, double sink,
                                                                double eps) {
 #pragma clang fp contract(off)
+  // The row's x and g stay in registers as their raw 16-byte chunks and are unpacked where used;
+  // one float per element, w = 8 r rho^8, carries the octic between passes.  sum(p g) is taken
+  // as sum(rho^8 g) / (sum rho^8 + sink) in the pass that forms sum rho^8, so three wave
+  // reductions serve the row, and the kernel holds few enough registers for six or more waves
+  // per SIMD to keep loads in flight.
   constexpr int EPC = Chunk<DT>::EPC;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const int64_t base = row * n;
   const float inv_n = 1.f / (float)n;
-  float z[NCH][8], gv[NCH][8], p[NCH][8], rr[NCH][8];
+  const int esz = DT == AFA_F32 ? 4 : 2;
+  u32x4_t xr[NCH], gr[NCH];
+  float w[NCH][8];
+  auto unpack = [&](const u32x4_t& c, float (&v)[8]) {
+    if constexpr (DT == AFA_F32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const unsigned u = c[i];
+        v[i] = __builtin_bit_cast(float, u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = Elem<DT>::lo(c[i]);
+        v[2 * i + 1] = Elem<DT>::hi(c[i]);
+      }
+    }
+  };
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int64_t e0 = (int64_t)(lane + 64 * j) * EPC;
     if (e0 < n) {
-      Chunk<DT>::load(x, base + e0, z[j]);
-      Chunk<DT>::load(g, base + e0, gv[j]);
+      xr[j] = *(const u32x4_t*)((const char*)x + (base + e0) * esz);
+      gr[j] = *(const u32x4_t*)((const char*)g + (base + e0) * esz);
+      float z[8];
+      unpack(xr[j], z);
 #pragma unroll
-      for (int i = 0; i < EPC; ++i) ss += z[j][i] * z[j][i];
+      for (int i = 0; i < EPC; ++i) ss += z[i] * z[i];
     }
   }
   ss = wave_sum(ss);
   const float tau = inv_sqrt(ss * inv_n + (float)eps);
-  float ks = 0.f;
+  float ks = 0.f, pg = 0.f;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     if ((int64_t)(lane + 64 * j) * EPC < n) {
+      float z[8], gv[8];
+      unpack(xr[j], z);
+      unpack(gr[j], gv);
 #pragma unroll
       for (int i = 0; i < EPC; ++i) {
-        z[j][i] = z[j][i] * tau;
-        p[j][i] = octic_hw(z[j][i], rr[j][i]);
-        ks += p[j][i];
+        float r;
+        const float p = octic_hw(z[i] * tau, r);
+        ks += p;
+        pg += p * gv[i];
+        w[j][i] = 8.f * r * p;
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // one chunk's unpacked values live at a time
   }
   ks = wave_sum(ks);
+  pg = wave_sum(pg);
   const float inv = 1.0f / (ks + (float)sink);
-  float dot = 0.f;
-#pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    if ((int64_t)(lane + 64 * j) * EPC < n) {
-#pragma unroll
-      for (int i = 0; i < EPC; ++i) {
-        p[j][i] = p[j][i] * inv;
-        dot += p[j][i] * gv[j][i];
-      }
-    }
-  }
-  dot = wave_sum(dot);
+  const float dot = pg * inv;
   float rad = 0.f;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     if ((int64_t)(lane + 64 * j) * EPC < n) {
+      float z[8], gv[8];
+      unpack(xr[j], z);
+      unpack(gr[j], gv);
 #pragma unroll
       for (int i = 0; i < EPC; ++i) {
-        gv[j][i] = 8.f * rr[j][i] * p[j][i] * (gv[j][i] - dot);  // ng
-        rad += gv[j][i] * z[j][i];
+        w[j][i] = w[j][i] * inv * (gv[i] - dot);  // ng
+        rad += w[j][i] * (z[i] * tau);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
   rad = wave_sum(rad) * inv_n;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int64_t e0 = (int64_t)(lane + 64 * j) * EPC;
     if (e0 < n) {
+      float z[8];
+      unpack(xr[j], z);
 #pragma unroll
-      for (int i = 0; i < EPC; ++i) gv[j][i] = tau * (gv[j][i] - rad * z[j][i]);
-      Chunk<DT>::store(dx, base + e0, gv[j]);
+      for (int i = 0; i < EPC; ++i) w[j][i] = tau * (w[j][i] - rad * (z[i] * tau));
+      Chunk<DT>::store(dx, base + e0, w[j]);
     }
   }
 }
