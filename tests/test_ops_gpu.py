@@ -419,3 +419,42 @@ def test_fused_rotation_equals_explicit_rotation_fp32():
     qr, kr = A.apply_ago_rotations(q, k, rot)
     explicit = A.pallas_afa_forward(qr, kr, v, causal=True)
     assert normwise(to_f64(fused), to_f64(explicit)) <= 1e-6
+
+
+@pytest.mark.parametrize("shape,rot", [((1, 2, 65536, 64), True), ((1, 1, 32768, 128), False)])
+def test_long_sequence_prefix_locality(shape, rot):
+    """Causal attention at long lengths (the 256-query kernel at 65536 keys, the 128-query
+    pipelined kernel at head_dim 128): the first 512 outputs and the first 512 rows of dq depend
+    only on the first 512 keys, so they match the 512-long problem, which the C contract checks.
+    dk and dv, which depend on every later query, must be finite; the default schedule is also
+    checked against the fully fused kernel over the whole length."""
+    from algebraic_intelligence_amd import _lib
+    B, H, L, D = shape
+    P = 512
+    q, k, v = make_qkv(shape, torch.bfloat16, seed=L + D)
+    g = make_qkv(shape, torch.bfloat16, seed=L + D + 1)[0]
+    freqs = 10000.0 ** (-2.0 * np.arange(D // 2) / D)
+    rot_l = A.build_cayley_rotary_matrix(D, L, freqs=freqs) if rot else None
+    rot_p = A.build_cayley_rotary_matrix(D, P, freqs=freqs) if rot else None
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, True, None, rot_l, 0, True)
+    out_s, _ = A.afa._launch_fwd(q, k, v, 0.5, True, None, rot_l, _lib.FLAG_SIMPLE_SCHEDULE, True)
+    assert torch.isfinite(out.float()).all() and torch.isfinite(den).all()
+    assert normwise(to_f64(out), to_f64(out_s)) <= 8e-3
+    qp, kp, vp, gp = (t[:, :, :P].contiguous() for t in (q, k, v, g))
+    out_p, den_p = A.afa._launch_fwd(qp, kp, vp, 0.5, True, None, rot_p, 0, True)
+    assert normwise(to_f64(out[:, :, :P]), to_f64(out_p)) <= 8e-3
+    assert normwise(to_f64(den[:, :, :P]), to_f64(den_p)) <= 1e-5
+    tabs = None if rot_p is None else (rot_p.c.detach().cpu().numpy().astype(np.float32),
+                                        rot_p.s.detach().cpu().numpy().astype(np.float32))
+    c_out, _ = C.afa_fwd(to_bits(qp), to_bits(kp), to_bits(vp), C.DT_BF16, 0.5, True, None, tabs)
+    assert normwise(to_f64(out_p), C.to_f32(c_out, C.DT_BF16)) <= 8e-3
+    rt = None if rot_l is None else (rot_l.c.contiguous(), rot_l.s.contiguous())
+    rtp = None if rot_p is None else (rot_p.c.contiguous(), rot_p.s.contiguous())
+    dq, dk, dv = _bwd_flags(q, k, v, out, den, g, True, None, 0, rot=rt)
+    for t in (dq, dk, dv):
+        assert torch.isfinite(t.float()).all()
+    pq, pk, pv = _bwd_flags(qp, kp, vp, out_p, den_p, gp, True, None, 0, rot=rtp)
+    e = normwise(to_f64(dq[:, :, :P]), to_f64(pq))
+    print(f"{shape} rot={rot}: out prefix vs 512-long {normwise(to_f64(out[:, :, :P]), to_f64(out_p)):.2e}, "
+          f"dq prefix {e:.2e}")
+    assert e <= 1e-2
