@@ -173,11 +173,13 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     // AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel where it exists
     if (pipe_ok && !(fused_ok && (flags & AFA_FLAG_SIMPLE_SCHEDULE))) {
       afa::FwdArgs b = a;
-      // head_dim 64: 256-query workgroups at two per CU (afa_fwd_d64.hip) when there are at least
-      // that many workgroups; otherwise, and at the other head dims, 128-query workgroups with
-      // several waves per SIMD (afa_fwd_pipe.hip)
+      // head_dim 64: 256-query workgroups at two per CU (afa_fwd_d64.hip) when they fill at least
+      // one and a half rounds of those slots; otherwise, and at the other head dims, 128-query
+      // workgroups with several waves per SIMD (afa_fwd_pipe.hip).  With a single round (C4: 512
+      // workgroups on 256 CUs) the finer causal blocks of the 128-query kernel balance better:
+      // 0.0545 against 0.0560 ms, measured on one box.
       const int64_t nwg256 = (int64_t)b.B * b.H * ((seq_len + 255) / 256);
-      const bool wide = head_dim == 64 && nwg256 >= 2 * (int64_t)cu_count();
+      const bool wide = head_dim == 64 && nwg256 >= 3 * (int64_t)cu_count();
       // with rotary tables k is rotated once into stream-ordered scratch; without that scratch
       // the fully fused kernel below (head_dim 64, 128) or the generic one rotates at tile load
       void* krot = nullptr;

@@ -231,7 +231,7 @@ def test_pipelined_d64_edge_shapes(shape, causal, valid, rot, dt, wide):
     are not tile multiples, tiny lengths, valid_len tails and odd batch x head counts (so the
     workgroup remap sees counts not divisible by 8).  Small grids take the 32-query kernel
     (afa_fwd_pipe.hip); `wide` repeats the heads until the 256-query workgroups number at least
-    two per CU, which takes afa_fwd_d64.hip, and checks every copy of a head is bitwise equal."""
+    three per CU, which takes afa_fwd_d64.hip, and checks every copy of a head is bitwise equal."""
     B, H, L, D = shape
     scale = 1.0 if dt == torch.bfloat16 else 0.4
     q, k, v = make_qkv(shape, dt, seed=sum(shape), scale=scale)
@@ -239,7 +239,7 @@ def test_pipelined_d64_edge_shapes(shape, causal, valid, rot, dt, wide):
     c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid, rotary=rotary)
     reps = 1
     if wide:
-        reps = -(-2 * _cu_count() // (B * H * -(-L // 256)))
+        reps = -(-3 * _cu_count() // (B * H * -(-L // 256)))
         q, k, v = (x.repeat(1, reps, 1, 1).contiguous() for x in (q, k, v))
     a, da = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
     b, db = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_SIMPLE_SCHEDULE)
