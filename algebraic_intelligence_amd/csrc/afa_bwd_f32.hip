@@ -479,7 +479,9 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dkdv_kernel(const GenArgs a) 
   }
 }
 
-bool f32_bwd_supported(int head_dim) { return head_dim == 32 || head_dim == 64 || head_dim == 128; }
+bool f32_bwd_supported(int head_dim) {
+  return head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128;
+}
 
 template <int D, bool ROT>
 static void f32_bwd_launch_d(const GenArgs& a, hipStream_t st) {
@@ -499,6 +501,7 @@ hipError_t f32_bwd_launch(const GenArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(afa_bwd_f32_prep_kernel, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, st, a);
   if (a.D == 32) f32_bwd_launch_r<32>(a, st);
   else if (a.D == 64) f32_bwd_launch_r<64>(a, st);
+  else if (a.D == 96) f32_bwd_launch_r<96>(a, st);
   else f32_bwd_launch_r<128>(a, st);
   return hipGetLastError();
 }

@@ -263,7 +263,9 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_combine_kernel(const FwdArgs 
   if (a.denom != nullptr && c4 == 0) a.denom[row] = tot;
 }
 
-bool f32_fwd_supported(int head_dim) { return head_dim == 32 || head_dim == 64 || head_dim == 128; }
+bool f32_fwd_supported(int head_dim) {
+  return head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128;
+}
 
 size_t f32_fwd_part_floats(const FwdArgs& a, int head_dim, int nsplit) {
   return (size_t)nsplit * a.B * a.H * a.L * (head_dim + 1);
@@ -296,6 +298,7 @@ hipError_t f32_fwd_launch(int head_dim, FwdArgs a, int nsplit, hipStream_t st) {
   a.nqb = (a.L + 127) / 128;
   if (head_dim == 32) return f32_launch_d<32>(a, nsplit, st);
   if (head_dim == 64) return f32_launch_d<64>(a, nsplit, st);
+  if (head_dim == 96) return f32_launch_d<96>(a, nsplit, st);
   return f32_launch_d<128>(a, nsplit, st);
 }
 
