@@ -96,12 +96,13 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_prep_kernel(const GenArgs a) 
 // ------------------------------------------------------------------------------ dQ
 template <int D, bool ROT>
 __global__ __launch_bounds__(256) void afa_bwd_f32_dq_kernel(const GenArgs a) {
-  constexpr int LDR = D + 4;   // padded LDS row: consecutive rows shift by 16 bytes
+  constexpr int DV = (D + 31) / 32 * 32;  // features in 32-feature output blocks (48 -> 64)
+  constexpr int LDR = DV + 4;  // padded LDS row (shifts 16 bytes per row); features [D, DV) zero
   constexpr int KH = D / 2;
-  constexpr int NDB = D / 32;
+  constexpr int NDB = DV / 32;
   constexpr int KJOBS = FKT * (D / 2) / 256;  // K rotation pairs per thread per tile
-  constexpr int VJOBS = FKT * (D / 4) / 256;  // float4 of V per thread per tile
-  static_assert(KJOBS >= 1 && VJOBS >= 1, "head_dim too small for the tile loader");
+  constexpr int VJOBS = (FKT * (D / 4) + 255) / 256;  // float4 of V per thread per tile
+  static_assert(FKT * (D / 2) % 256 == 0 && KJOBS >= 1, "head_dim does not fit the tile loader");
   __shared__ __attribute__((aligned(16))) float ks[2][FKT * LDR];
   __shared__ __attribute__((aligned(16))) float vs[2][FKT * LDR];
 
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dq_kernel(const GenArgs a) {
       const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
       const int key = t * FKT + r;
       f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-      vx[i] = key < L ? *(const f32x4_t*)(vp + (int64_t)key * D + 4 * c4) : z;
+      vx[i] = key < L && e < FKT * (D / 4) ? *(const f32x4_t*)(vp + (int64_t)key * D + 4 * c4) : z;
     }
   };
   auto store = [&](int buf) {
@@ -195,9 +196,16 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dq_kernel(const GenArgs a) {
 #pragma unroll
     for (int i = 0; i < VJOBS; ++i) {
       const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
-      *(f32x4_t*)&vs[buf][r * LDR + 4 * c4] = vx[i];
+      if (e < FKT * (D / 4)) *(f32x4_t*)&vs[buf][r * LDR + 4 * c4] = vx[i];
     }
   };
+  if constexpr (DV > D) {  // the padding features of every K and V row, once
+    for (int e = tid; e < 2 * FKT * (DV - D); e += 256) {
+      const int buf = e / (FKT * (DV - D)), r = (e / (DV - D)) % FKT, f = D + e % (DV - D);
+      ks[buf][r * LDR + f] = 0.f;
+      vs[buf][r * LDR + f] = 0.f;
+    }
+  }
 
   f32x16_t dq[NDB];
 #pragma unroll
@@ -266,11 +274,13 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dq_kernel(const GenArgs a) {
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int m = db * 32 + 8 * e4 + 4 * g;  // features m .. m+3 (two rotation pairs)
-        if constexpr (ROT) f_unrotate4<D>(dq[db], 4 * e4, rc, rs, qi, m);
-        f32x4_t w;
+        if (DV == D || m < D) {
+          if constexpr (ROT) f_unrotate4<D>(dq[db], 4 * e4, rc, rs, qi, m);
+          f32x4_t w;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = dq[db][4 * e4 + u];
-        *(f32x4_t*)(op + m) = w;
+          for (int u = 0; u < 4; ++u) w[u] = dq[db][4 * e4 + u];
+          *(f32x4_t*)(op + m) = w;
+        }
       }
   }
 }
@@ -278,12 +288,13 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dq_kernel(const GenArgs a) {
 // ------------------------------------------------------------------------------ dK, dV
 template <int D, bool ROT>
 __global__ __launch_bounds__(256) void afa_bwd_f32_dkdv_kernel(const GenArgs a) {
-  constexpr int LDR = D + 4;
+  constexpr int DV = (D + 31) / 32 * 32;  // features in 32-feature output blocks (48 -> 64)
+  constexpr int LDR = DV + 4;  // features [D, DV) of the q and g rows stay zero
   constexpr int KH = D / 2;
-  constexpr int NDB = D / 32;
+  constexpr int NDB = DV / 32;
   constexpr int QJOBS = FKT * (D / 2) / 256;  // Q rotation pairs per thread per tile
-  constexpr int GJOBS = FKT * (D / 4) / 256;  // float4 of g per thread per tile
-  static_assert(QJOBS >= 1 && GJOBS >= 1, "head_dim too small for the tile loader");
+  constexpr int GJOBS = (FKT * (D / 4) + 255) / 256;  // float4 of g per thread per tile
+  static_assert(FKT * (D / 2) % 256 == 0 && QJOBS >= 1, "head_dim does not fit the tile loader");
   __shared__ __attribute__((aligned(16))) float qs[2][FKT * LDR];
   __shared__ __attribute__((aligned(16))) float gs[2][FKT * LDR];
   __shared__ float es[2][2 * FKT];  // E, then 1/d of the tile's rows
@@ -361,7 +372,7 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dkdv_kernel(const GenArgs a) 
       const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
       const int row = t * FKT + r;
       f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-      gx[i] = row < L ? *(const f32x4_t*)(gp + (int64_t)row * D + 4 * c4) : z;
+      gx[i] = row < L && e < FKT * (D / 4) ? *(const f32x4_t*)(gp + (int64_t)row * D + 4 * c4) : z;
     }
     if (tid < 2 * FKT) {
       const int row = t * FKT + (tid & (FKT - 1));
@@ -383,10 +394,17 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dkdv_kernel(const GenArgs a) 
 #pragma unroll
     for (int i = 0; i < GJOBS; ++i) {
       const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
-      *(f32x4_t*)&gs[buf][r * LDR + 4 * c4] = gx[i];
+      if (e < FKT * (D / 4)) *(f32x4_t*)&gs[buf][r * LDR + 4 * c4] = gx[i];
     }
     if (tid < 2 * FKT) es[buf][tid] = ex;
   };
+  if constexpr (DV > D) {  // the padding features of every q and g row, once
+    for (int e = tid; e < 2 * FKT * (DV - D); e += 256) {
+      const int buf = e / (FKT * (DV - D)), r = (e / (DV - D)) % FKT, f = D + e % (DV - D);
+      qs[buf][r * LDR + f] = 0.f;
+      gs[buf][r * LDR + f] = 0.f;
+    }
+  }
 
   f32x16_t dk[NDB], dv[NDB];
 #pragma unroll
@@ -466,21 +484,23 @@ __global__ __launch_bounds__(256) void afa_bwd_f32_dkdv_kernel(const GenArgs a) 
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int m = db * 32 + 8 * e4 + 4 * g;
-        if constexpr (ROT) f_unrotate4<D>(dk[db], 4 * e4, rc, rs, kj, m);
-        f32x4_t wk, wv;
+        if (DV == D || m < D) {
+          if constexpr (ROT) f_unrotate4<D>(dk[db], 4 * e4, rc, rs, kj, m);
+          f32x4_t wk, wv;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          wk[u] = dk[db][4 * e4 + u];
-          wv[u] = dv[db][4 * e4 + u];
+          for (int u = 0; u < 4; ++u) {
+            wk[u] = dk[db][4 * e4 + u];
+            wv[u] = dv[db][4 * e4 + u];
+          }
+          *(f32x4_t*)(kout + m) = wk;
+          *(f32x4_t*)(vout + m) = wv;
         }
-        *(f32x4_t*)(kout + m) = wk;
-        *(f32x4_t*)(vout + m) = wv;
       }
   }
 }
 
 bool f32_bwd_supported(int head_dim) {
-  return head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128;
+  return head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128;
 }
 
 template <int D, bool ROT>
@@ -500,6 +520,7 @@ hipError_t f32_bwd_launch(const GenArgs& a, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.H * a.L;
   hipLaunchKernelGGL(afa_bwd_f32_prep_kernel, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, st, a);
   if (a.D == 32) f32_bwd_launch_r<32>(a, st);
+  else if (a.D == 48) f32_bwd_launch_r<48>(a, st);
   else if (a.D == 64) f32_bwd_launch_r<64>(a, st);
   else if (a.D == 96) f32_bwd_launch_r<96>(a, st);
   else f32_bwd_launch_r<128>(a, st);

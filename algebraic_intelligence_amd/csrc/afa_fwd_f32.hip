@@ -44,13 +44,15 @@ __device__ __forceinline__ float rot_second(float c, float s, float x0, float x1
 template <int D, bool ROT, bool SPLIT>
 __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
   constexpr int LDR = D + 4;   // padded LDS row: consecutive rows shift by 16 bytes (no conflicts)
+  constexpr int DV = (D + 31) / 32 * 32;  // V features in 32-feature output blocks (48 -> 64)
+  constexpr int LDV = DV + 4;  // V rows; features [D, DV) stay zero
   constexpr int KH = D / 2;    // head_dim entries per lane group
-  constexpr int NDB = D / 32;  // 32-feature output blocks
+  constexpr int NDB = DV / 32; // 32-feature output blocks
   constexpr int KJOBS = KT * (D / 2) / 256;  // rotation pairs per thread per tile
-  constexpr int VJOBS = KT * (D / 4) / 256;  // float4 of V per thread per tile
-  static_assert(KJOBS >= 1 && VJOBS >= 1, "head_dim too small for the tile loader");
+  constexpr int VJOBS = (KT * (D / 4) + 255) / 256;  // float4 of V per thread per tile
+  static_assert(KT * (D / 2) % 256 == 0 && KJOBS >= 1, "head_dim does not fit the tile loader");
   __shared__ __attribute__((aligned(16))) float ks[2][KT * LDR];
-  __shared__ __attribute__((aligned(16))) float vs[2][KT * LDR];
+  __shared__ __attribute__((aligned(16))) float vs[2][KT * LDV];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
       const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
       const int key = t * KT + r;
       f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-      vx[i] = key < L ? *(const f32x4_t*)(vp + (int64_t)key * a.v_l + 4 * c4) : z;
+      vx[i] = key < L && e < KT * (D / 4) ? *(const f32x4_t*)(vp + (int64_t)key * a.v_l + 4 * c4) : z;
     }
   };
   auto store = [&](int buf) {
@@ -140,9 +142,15 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
 #pragma unroll
     for (int i = 0; i < VJOBS; ++i) {
       const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
-      *(f32x4_t*)&vs[buf][r * LDR + 4 * c4] = vx[i];
+      if (e < KT * (D / 4)) *(f32x4_t*)&vs[buf][r * LDV + 4 * c4] = vx[i];
     }
   };
+  if constexpr (DV > D) {  // the padding features of both V buffers, once
+    for (int e = tid; e < 2 * KT * (DV - D); e += 256) {
+      const int buf = e / (KT * (DV - D)), r = (e / (DV - D)) % KT, f = D + e % (DV - D);
+      vs[buf][r * LDV + f] = 0.f;
+    }
+  }
 
   f32x16_t o[NDB];
 #pragma unroll
@@ -189,7 +197,7 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int kr = 8 * (j >> 2) + 4 * g + (j & 3);
-          o[db] = mma_f32(vt[kr * LDR + db * 32 + l32], st[j], o[db]);
+          o[db] = mma_f32(vt[kr * LDV + db * 32 + l32], st[j], o[db]);
         }
     }
     // the buffer of tile t+1 was last read in tile t-1, before the previous barrier
@@ -210,10 +218,12 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
-          f32x4_t w;
+          if (DV == D || db * 32 + 8 * e4 + 4 * g < D) {
+            f32x4_t w;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u];
-          *(f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g) = w;
+            for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u];
+            *(f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g) = w;
+          }
         }
       if (g == 0) pd[(int64_t)bh * L + qi] = dsum;
     }
@@ -226,10 +236,12 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
-        f32x4_t w;
+        if (DV == D || db * 32 + 8 * e4 + 4 * g < D) {
+          f32x4_t w;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u] / tot;
-        *(f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g) = w;
+          for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u] / tot;
+          *(f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g) = w;
+        }
       }
     if (a.denom != nullptr && g == 0) a.denom[(int64_t)bh * L + qi] = tot;
   }
@@ -264,7 +276,7 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_combine_kernel(const FwdArgs 
 }
 
 bool f32_fwd_supported(int head_dim) {
-  return head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128;
+  return head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128;
 }
 
 size_t f32_fwd_part_floats(const FwdArgs& a, int head_dim, int nsplit) {
@@ -297,6 +309,7 @@ static hipError_t f32_launch_d(const FwdArgs& a, int nsplit, hipStream_t st) {
 hipError_t f32_fwd_launch(int head_dim, FwdArgs a, int nsplit, hipStream_t st) {
   a.nqb = (a.L + 127) / 128;
   if (head_dim == 32) return f32_launch_d<32>(a, nsplit, st);
+  if (head_dim == 48) return f32_launch_d<48>(a, nsplit, st);
   if (head_dim == 64) return f32_launch_d<64>(a, nsplit, st);
   if (head_dim == 96) return f32_launch_d<96>(a, nsplit, st);
   return f32_launch_d<128>(a, nsplit, st);

@@ -301,6 +301,7 @@ def test_device_lds_limit_reported():
     ((1, 2, 130, 32), True, None, True), ((2, 1, 392, 128), False, 300, False),
     ((1, 2, 256, 128), True, None, True), ((3, 5, 129, 64), True, None, False),
     ((1, 2, 300, 96), True, None, True), ((2, 1, 200, 96), False, 150, False),
+    ((1, 2, 260, 48), True, None, True), ((3, 1, 129, 48), False, 100, False),
 ])
 @pytest.mark.parametrize("wide", [False, True])
 def test_fp32_mfma_vs_generic_and_fp64(shape, causal, valid, rot, wide):

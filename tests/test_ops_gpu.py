@@ -196,6 +196,7 @@ def test_mfma_backward_with_rotary_tables(shape, causal, valid, dt):
     ((1, 2, 256, 64), True, None, False), ((2, 3, 200, 64), False, None, True), ((1, 2, 300, 32), True, 257, False),
     ((1, 1, 7, 32), True, None, True), ((1, 2, 256, 128), True, None, True), ((2, 1, 130, 128), False, 100, False),
     ((1, 2, 300, 96), True, None, True), ((2, 1, 140, 96), False, 99, False),
+    ((1, 2, 260, 48), True, None, True), ((3, 1, 129, 48), False, 100, False),
 ])
 def test_fp32_mfma_backward(shape, causal, valid, rot):
     """The fp32 backward on the fp32 matrix cores against the generic fp32 kernel (forced with
