@@ -152,3 +152,24 @@ def test_oace_rejects_invalid_arguments(lib):
                                      None) == _lib.ERR_GAMMA
     assert lib.oace_softmax_loss_bwd(_lib.AFA_F32, 4, 9, DUMMY, DUMMY, 2.0, None, None, DUMMY,
                                      None) == _lib.ERR_NULL
+
+
+def test_python_constants_match_the_header():
+    """Every #define and enum value the Python layer copies (dtype codes, AFA and OACE flags,
+    weight layouts, row record width) equals the header's."""
+    from algebraic_intelligence_amd import oace
+    text = open(HEADER).read()
+    defs = {m.group(1): int(m.group(2), 0) for m in re.finditer(r"#define\s+(\w+)\s+(0x[0-9a-fA-F]+|\d+)u?\b", text)}
+    enum = {m.group(1): int(m.group(2)) for m in re.finditer(r"\b(AFA_(?:F32|BF16|F16|F64))\s*=\s*(\d+)", text)}
+    assert enum == {"AFA_F32": _lib.AFA_F32, "AFA_BF16": _lib.AFA_BF16, "AFA_F16": _lib.AFA_F16, "AFA_F64": _lib.AFA_F64}
+    pairs = {
+        "AFA_FLAG_EXACT_TAIL": _lib.FLAG_EXACT_TAIL, "AFA_FLAG_GENERIC": _lib.FLAG_GENERIC,
+        "AFA_FLAG_EXACT_REF": _lib.FLAG_EXACT_REF, "AFA_FLAG_SIMPLE_SCHEDULE": _lib.FLAG_SIMPLE_SCHEDULE,
+        "OACE_W_DV": oace.OACE_W_DV, "OACE_W_VD": oace.OACE_W_VD, "OACE_ROW_FIELDS": oace.ROW_FIELDS,
+        "OACE_FLAG_WT_READY": oace.FLAG_WT_READY, "OACE_FLAG_Z_READY": oace.FLAG_Z_READY,
+        "OACE_FLAG_RECOMPUTE_Z": oace.FLAG_RECOMPUTE_Z,
+    }
+    for name, value in pairs.items():
+        assert defs[name] == value, name
+    flags = [v for k, v in defs.items() if "_FLAG_" in k]
+    assert len(set(flags)) == len(flags)  # every flag its own bit
