@@ -162,26 +162,32 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
   const bool vtail = v0 + TV > a.V;
   float* red = (float*)lds;  // the ring is idle after the last barrier
   if constexpr (MODE == MODE_SQZ) {
-    // the logits themselves, 4 consecutive vocabulary entries per store (a group that starts
-    // below V ends below the padded row length; its entries past V are finite and never read)
+    // the logits themselves, 32 rows at a time through LDS (the idle ring): each wave writes its
+    // 64 vocabulary columns of the 32 rows, then every wave stores whole 1 KB row segments
+    // (a 4-entry group that starts below V ends below the padded row length; its entries past V
+    // are finite and never read)
+    constexpr int ZP = TV + 4;  // staged row pitch in floats (16-byte aligned rows)
+    static_assert(32 * ZP * 4 <= NSTAGE * STAGE, "the staged rows must fit the ring");
+    float* zt = (float*)lds;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const int n = n0 + nb * 32 + l32;
-      if (n < a.N) {
-        float* zrow = a.zc + (int64_t)n * a.ldz;
 #pragma unroll
-        for (int vb = 0; vb < 2; ++vb)
+      for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
-          for (int e4 = 0; e4 < 4; ++e4) {
-            const int vs = vw + 32 * vb + 8 * e4 + 4 * g;
-            if (vs < a.V) {
-              f32x4_t w;
+        for (int e4 = 0; e4 < 4; ++e4) {
+          f32x4_t w;
 #pragma unroll
-              for (int u = 0; u < 4; ++u) w[u] = acc[vb][nb][4 * e4 + u];
-              *(f32x4_t*)(zrow + vs) = w;
-            }
-          }
+          for (int u = 0; u < 4; ++u) w[u] = acc[vb][nb][4 * e4 + u];
+          *(f32x4_t*)(zt + l32 * ZP + wave * 64 + 32 * vb + 8 * e4 + 4 * g) = w;
+        }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 32 * TV / 4 / 256; ++i) {
+        const int idx = tid + 256 * i, row = idx / (TV / 4), c4 = idx % (TV / 4);
+        const int n = n0 + nb * 32 + row, vs = v0 + 4 * c4;
+        if (n < a.N && vs < a.V) *(f32x4_t*)(a.zc + (int64_t)n * a.ldz + vs) = *(const f32x4_t*)(zt + row * ZP + 4 * c4);
       }
+      __syncthreads();
     }
   }
   if constexpr (MODE == MODE_SQ || MODE == MODE_SQZ) {
