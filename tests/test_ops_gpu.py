@@ -460,3 +460,35 @@ def test_long_sequence_prefix_locality(shape, rot):
     print(f"{shape} rot={rot}: out prefix vs 512-long {normwise(to_f64(out[:, :, :P]), to_f64(out_p)):.2e}, "
           f"dq prefix {e:.2e}")
     assert e <= 1e-2
+
+
+@pytest.mark.parametrize("shape,rot", [((2, 16, 8192, 128), False), ((8, 12, 4096, 64), True)])
+def test_backward_linearity_full_size(shape, rot):
+    """At the full C5 and C3 (Cayley tables) sizes, the backward is linear in the output
+    cotangent g: doubling g doubles dq, dk and dv bit for bit (every product and the bf16
+    rounding of ds scale exactly by 2), and for g1, g2 whose sum bf16 holds exactly,
+    d(g1 + g2) = d(g1) + d(g2) up to the rounding of ds."""
+    B, H, L, D = shape
+    q, k, v = make_qkv(shape, torch.bfloat16, seed=L + D + 5)
+    rt = None
+    rot_obj = None
+    if rot:
+        rot_obj = A.build_cayley_rotary_matrix(D, L, freqs=10000.0 ** (-2.0 * np.arange(D // 2) / D))
+        rt = (rot_obj.c.contiguous(), rot_obj.s.contiguous())
+    out, den = A.afa._launch_fwd(q, k, v, 0.5, True, None, rot_obj, 0, True)
+    gen = torch.Generator(device=DEV).manual_seed(L)
+    # multiples of 1/16 in [-4, 4]: sums of two stay exact in bf16
+    g1 = (torch.randint(-64, 65, shape, generator=gen, device=DEV).float() / 16).to(torch.bfloat16)
+    g2 = (torch.randint(-64, 65, shape, generator=gen, device=DEV).float() / 16).to(torch.bfloat16)
+    g12 = (g1.float() + g2.float()).to(torch.bfloat16)
+    assert torch.equal(g12.float(), g1.float() + g2.float())
+    d1 = _bwd_flags(q, k, v, out, den, g1, True, None, 0, rot=rt)
+    d2 = _bwd_flags(q, k, v, out, den, g2, True, None, 0, rot=rt)
+    d12 = _bwd_flags(q, k, v, out, den, g12, True, None, 0, rot=rt)
+    dd = _bwd_flags(q, k, v, out, den, (2 * g1.float()).to(torch.bfloat16), True, None, 0, rot=rt)
+    for name, a1, a2, a12, a2x in zip(("dq", "dk", "dv"), d1, d2, d12, dd):
+        assert torch.isfinite(a12.float()).all(), name
+        assert torch.equal(a2x.float(), 2 * a1.float()), name
+        e = normwise(to_f64(a12), to_f64(a1) + to_f64(a2))
+        print(f"{shape} rot={rot} {name}: d(g1+g2) vs d(g1)+d(g2) {e:.2e}")
+        assert e <= 1e-2, name
