@@ -67,7 +67,7 @@ __device__ __forceinline__ int swap23(int j) { return (j & ~12) | ((j & 4) << 1)
 // 1: s = sqrt(2) x evaluated as (rho/sqrt 2)^8 = rho^8/16 (bf16 only: weights and sink carry 1/16);
 // 2: s = sqrt(2) x formed explicitly.
 template <int DT, int D, int QW, bool EXACT, int SM, bool ROT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1, D <= 128 ? 2 : 1)))
 void afa_fwd_mfma_kernel(const FwdArgs a) {
   constexpr int KT = 64;             // keys per LDS tile
   constexpr int NQB = QW / 32;       // 32-query column blocks per wave
@@ -306,7 +306,7 @@ static hipError_t launch_rot(const FwdArgs& a, hipStream_t stream) {
 int mfma_fwd_queries_per_block(int head_dim) { return head_dim == 64 ? 256 : 128; }
 
 bool mfma_fwd_supported(int dtype, int head_dim) {
-  return (dtype == AFA_BF16 || dtype == AFA_F16) && (head_dim == 64 || head_dim == 128);
+  return (dtype == AFA_BF16 || dtype == AFA_F16) && (head_dim == 64 || head_dim == 128 || head_dim == 256);
 }
 
 hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream) {
@@ -323,6 +323,13 @@ hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
                  : launch_rot<AFA_F16, 64, 64, false, 0>(a, stream);
   }
   a.q_scale = 0.0625f;
+  if (head_dim == 256) {  // 1/sqrt(256) = 2^-4, exact in q
+    if (dtype == AFA_BF16)
+      return exact ? launch_rot<AFA_BF16, 256, 32, true, 0>(a, stream)
+                   : launch_rot<AFA_BF16, 256, 32, false, 0>(a, stream);
+    return exact ? launch_rot<AFA_F16, 256, 32, true, 0>(a, stream)
+                 : launch_rot<AFA_F16, 256, 32, false, 0>(a, stream);
+  }
   if (dtype == AFA_BF16) {
     if (exact) return launch_rot<AFA_BF16, 128, 32, true, 2>(a, stream);
     a.omega *= 0.0625f;

@@ -202,6 +202,31 @@ def test_head_dim_128(dt):
     assert normwise(to_f64(den), c_den) <= 1e-5
 
 
+@pytest.mark.parametrize("shape,causal,valid,rot", [
+    ((1, 2, 300, 256), True, None, True), ((2, 1, 200, 256), False, 150, False), ((1, 1, 1, 256), True, None, False),
+    ((1, 3, 513, 256), True, None, False),
+])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_head_dim_256(shape, causal, valid, rot, dt):
+    """head_dim 256 (the reference accepts multiples of 128 above 128) on the fully fused MFMA
+    kernel, 1/sqrt(256) = 2^-4 folded into q: against the generic kernel, the C contract and
+    float64.  fp16 inputs are scaled to keep the fp16 weights below overflow."""
+    B, H, L, D = shape
+    q, k, v = make_qkv(shape, dt, seed=sum(shape), scale=1.0 if dt == torch.bfloat16 else 0.3)
+    rotary = A.build_cayley_rotary_matrix(D, L, freqs=_c3_freqs(D)) if rot else None
+    out, den = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary)
+    gout, gden = _fwd(q, k, v, causal=causal, valid=valid, rotary=rotary, flags=_lib.FLAG_GENERIC)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid_len=valid, rotary=rotary)
+    tol = _ulp_tol(dt)
+    e_g, e_c = normwise(to_f64(out), to_f64(gout)), normwise(to_f64(out), c_out)
+    print(f"D=256 {shape} causal={causal} valid={valid} rot={rot} {dt}: vs generic {e_g:.2e} vs contract {e_c:.2e}")
+    assert e_g <= tol and e_c <= tol
+    assert normwise(to_f64(den), c_den) <= 1e-5
+    if not rot:
+        ref = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, causal, valid_len=valid)
+        assert normwise(to_f64(out), ref) <= 2e-2
+
+
 @pytest.mark.parametrize("D", [8, 16, 32, 48, 96, 256])
 def test_generic_head_dims(D):
     q, k, v = make_qkv((1, 2, 96, D), torch.float32, seed=14)
