@@ -94,7 +94,9 @@ __device__ __forceinline__ u32x4_t frag_tr(const unsigned short* tile, int r0, i
 
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
-constexpr int padded_dim(int d) { return d <= 64 ? 64 : 128; }
+constexpr int padded_dim(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
+// Waves per SIMD of the dQ and dK/dV kernels by padded head dim.
+constexpr int bwd_waves(int dp) { return dp == 64 ? 3 : dp == 128 ? 2 : 1; }
 
 // Score factor after the folded 1/8: 8 fl(1/sqrt D) (a compile-time constant at D = 64, 128).
 template <int D>
@@ -211,8 +213,8 @@ __global__ __launch_bounds__(256) void afa_bwd_mfma_rotate_kernel(const GenArgs 
 
 // ------------------------------------------------------------------------------ dQ
 template <int DT, int D, bool EXACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(padded_dim(D) == 64 ? 3 : 2,
-                                                                     padded_dim(D) == 64 ? 3 : 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves(padded_dim(D)),
+                                                                     bwd_waves(padded_dim(D)))))
 void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   constexpr int DP = padded_dim(D);     // LDS row and MFMA width
   constexpr int KT = 64;
@@ -373,15 +375,15 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
 
 // ------------------------------------------------------------------------------ dK, dV
 template <int DT, int D, bool EXACT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(padded_dim(D) == 64 ? 3 : 2,
-                                                                     padded_dim(D) == 64 ? 3 : 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves(padded_dim(D)),
+                                                                     bwd_waves(padded_dim(D)))))
 void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   constexpr int DP = padded_dim(D);
   // The V rows of the workgroup's 128 keys stay in LDS instead of registers.  At DP = 128 (where
   // the k, v, dk, dv registers alone would take 192 VGPRs) the query tiles have 32 rows, so two
   // waves fit per SIMD and two workgroups per CU; at DP = 64, three of each.
   constexpr bool VLDS = true;
-  constexpr int QT = DP == 128 ? 32 : 64;
+  constexpr int QT = DP >= 128 ? 32 : 64;
   constexpr int SUBS = QT / 32;  // 32-query sub-tiles per tile
   constexpr int LPE = QT / 4;    // lanes loading E (and as many 1/d), 4 rows each
   constexpr int NCK = DP / 8;
@@ -590,7 +592,8 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
 // ------------------------------------------------------------------------------ launcher
 bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len) {
   return (dtype == AFA_BF16 || dtype == AFA_F16) &&
-         (head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128) &&
+         (head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 96 || head_dim == 128 ||
+          head_dim == 256) &&
          seq_len >= 1 && seq_len * head_dim < (int64_t(1) << 31);  // 32-bit in-head offsets
 }
 
@@ -630,6 +633,7 @@ static hipError_t bwd_launch_dt(const GenArgs& a, bool exact, void* rot_scratch,
     case 64: return bwd_launch_e<DT, 64>(a, exact, rot_scratch, st);
     case 96: return bwd_launch_e<DT, 96>(a, exact, rot_scratch, st);
     case 128: return bwd_launch_e<DT, 128>(a, exact, rot_scratch, st);
+    case 256: return bwd_launch_e<DT, 256>(a, exact, rot_scratch, st);
     default: return hipErrorInvalidValue;
   }
 }

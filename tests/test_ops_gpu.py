@@ -130,6 +130,7 @@ def _bwd_flags(q, k, v, out, den, g, causal, valid, flags, rot=None):
     ((1, 2, 300, 48), True, 257), ((1, 1, 8, 48), True, None), ((1, 2, 392, 96), True, None),
     ((2, 1, 200, 96), False, 150), ((1, 2, 257, 64), True, None), ((2, 1, 130, 128), False, 100),
     ((1, 1, 1, 64), True, None), ((1, 3, 3, 48), False, None), ((1, 2, 1001, 96), True, 999),
+    ((1, 2, 260, 256), True, None), ((2, 1, 130, 256), False, 100),
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_mfma_backward_vs_generic_and_contract(shape, causal, valid, dt):
@@ -161,7 +162,7 @@ def test_mfma_backward_vs_generic_and_contract(shape, causal, valid, dt):
 @pytest.mark.parametrize("shape,causal,valid", [
     ((1, 2, 256, 64), True, None), ((2, 3, 200, 64), False, None), ((1, 2, 1000, 64), True, 777),
     ((1, 2, 256, 128), True, None), ((2, 1, 392, 128), False, 300), ((1, 2, 200, 48), True, None),
-    ((1, 2, 300, 96), False, 257), ((1, 1, 128, 32), True, None),
+    ((1, 2, 300, 96), False, 257), ((1, 1, 128, 32), True, None), ((1, 2, 200, 256), True, None),
 ])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_mfma_backward_with_rotary_tables(shape, causal, valid, dt):
