@@ -65,10 +65,11 @@ int afa_version(void);
  * rot_cos/rot_sin (nullable, both or neither): Cayley rotary tables (rot_len, head_dim/2),
  * fp32 (fp64 for AFA_F64); q and k rows at position i are rotated by row i (fusing
  * _rotate_tensor, src/attention.py:142-152, as called from src/model.py:262-264): q when the
- * kernel loads it, k at tile load, except on the bf16/fp16 head_dim 64 and 128 paths, where k
- * is rotated once per call into batch*heads*seq_len*head_dim elements of stream-ordered scratch
- * (hipMallocAsync, freed on `stream` before the call returns; if that allocation fails the
- * fully fused kernel runs instead).  AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel.
+ * kernel loads it, k at tile load, except on the pipelined bf16/fp16 paths (head_dim 32, 48,
+ * 64, 96, 128), where k is rotated once per call into batch*heads*seq_len*head_dim elements of
+ * stream-ordered scratch (hipMallocAsync, freed on `stream` before the call returns; if that
+ * allocation fails the fully fused kernel runs instead at head_dim 64 and 128, the generic one
+ * otherwise).  AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel (head_dim 64, 128).
  */
 int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
             const void* q, const void* k, const void* v, const int64_t* strides, void* out,
@@ -81,9 +82,9 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
  * denom (= d_total, fp32; fp64 for AFA_F64) and the output cotangent g (same layout as q).
  * Outputs dq, dk, dv (contiguous).  With rotary tables the forward rotated q and k, and the
  * returned dq, dk are with respect to the unrotated inputs (the fp32 matrix-core kernels rotate
- * them as tiles are staged); on the bf16/fp16 matrix-core path
- * (head_dim 32, 48, 64, 96, 128) q and k are then rotated once into
- * 2*batch*heads*seq_len*head_dim elements of stream-ordered scratch (hipMallocAsync, freed on `stream` before the call returns; if that
+ * them as tiles are staged); on the bf16/fp16 matrix-core path (head_dim 32, 48, 64, 96, 128,
+ * 256) q and k are then rotated once into 2*batch*heads*seq_len*head_dim elements of
+ * stream-ordered scratch (hipMallocAsync, freed on `stream` before the call returns; if that
  * allocation fails the generic kernel runs instead).  workspace: at least
  * afa_bwd_workspace_size() bytes of device memory, or NULL to let the call allocate and free
  * it on `stream`.
