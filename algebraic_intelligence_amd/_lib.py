@@ -28,9 +28,10 @@ SIGNATURES = {
     "afa_status_string": (ctypes.c_char_p, [_int]),
     "afa_last_hip_error": (_int, []),
     "afa_version": (_int, []),
+    "afa_fwd_workspace_size": (_sz, [_int, _i64, _i64, _i64, _i64, _int]),
     "afa_fwd": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
-                       _dbl, _int, _i64, _uint, _vp]),
-    "afa_bwd_workspace_size": (_sz, [_int, _i64, _i64, _i64, _i64]),
+                       _dbl, _int, _i64, _uint, _vp, _sz, _vp]),
+    "afa_bwd_workspace_size": (_sz, [_int, _i64, _i64, _i64, _i64, _int]),
     "afa_bwd": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                        _vp, _vp, _i64, _dbl, _int, _i64, _uint, _vp, _sz, _vp]),
     "asoftmax_fwd": (_int, [_int, _i64, _i64, _vp, _vp, _dbl, _dbl, _vp]),
@@ -123,3 +124,19 @@ def check(rc: int, what: str) -> None:
     if rc in (ERR_UNSUPPORTED, ERR_ALIGN):
         raise NotImplementedError(f"{what}: {msg}")
     raise ValueError(f"{what}: {msg}")
+
+
+def table_2d(t: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """A (positions, head_dim/2) view of a Cayley table, broadcast axes of size 1 dropped.
+
+    The reference aligns the tables to the sequence axis and the pair axis and fails when their
+    shape does not fit the head dimension (src/attention.py:110-139); a table built for another
+    head dimension must not be reinterpreted as more rows here."""
+    if head_dim % 2 != 0:
+        raise ValueError(f"rotary tables need an even head dimension, got {head_dim}")
+    lead = [d for d in t.shape[:-1] if d != 1] if t.ndim >= 1 else []
+    if t.ndim == 0 or len(lead) > 1 or t.shape[-1] != head_dim // 2:
+        raise ValueError(
+            f"rotary tables must have shape (positions, head_dim/2) = (L, {head_dim // 2}) up to axes of "
+            f"size 1, got {tuple(t.shape)}")
+    return t.reshape(lead[0] if lead else 1, head_dim // 2)

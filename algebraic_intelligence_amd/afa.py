@@ -21,6 +21,7 @@ from typing import Optional, Tuple, Union
 import torch
 
 from . import _lib
+from ._lib import table_2d
 
 __all__ = [
     "pallas_afa_forward", "tiled_afa_forward", "exact_afa_reference", "exact_afa_with_denominator",
@@ -44,11 +45,11 @@ def _rotary_tables(rotary_params, q: torch.Tensor):
         raise TypeError(f"Unsupported rotary parameters type: {type(rotary_params)}")
     tdt = torch.float64 if q.dtype == torch.float64 else torch.float32
     D = q.shape[-1]
-    c = torch.as_tensor(c, device=q.device).to(tdt).reshape(-1, D // 2).contiguous()
-    s = torch.as_tensor(s, device=q.device).to(tdt).reshape(-1, D // 2).contiguous()
+    c = table_2d(torch.as_tensor(c, device=q.device), D)
+    s = table_2d(torch.as_tensor(s, device=q.device), D)
     if c.shape != s.shape:
         raise ValueError(f"rotary tables must match, got {tuple(c.shape)} and {tuple(s.shape)}")
-    return c, s, c.shape[0]
+    return c.to(tdt).contiguous(), s.to(tdt).contiguous(), c.shape[0]
 
 
 def _strides(*ts):
@@ -65,6 +66,7 @@ def _prep(t: torch.Tensor) -> torch.Tensor:
 
 def _launch_fwd(q, k, v, sink_omega, causal, valid_seq_len, rotary_params, flags,
                 want_denominator):
+    c, s, rot_len = _rotary_tables(rotary_params, q)  # shape checks first, as the reference's
     dev = _lib.require_device(q, k, v)
     dt = _lib.dtype_code(q.dtype)
     if k.dtype != q.dtype or v.dtype != q.dtype:
@@ -73,13 +75,15 @@ def _launch_fwd(q, k, v, sink_omega, causal, valid_seq_len, rotary_params, flags
     B, H, L, D = q.shape
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=dev)
     den = torch.empty((B, H, L, 1), dtype=_lib.accum_dtype(q.dtype), device=dev) if want_denominator else None
-    c, s, rot_len = _rotary_tables(rotary_params, q)
     with torch.cuda.device(dev):
+        # the workspace comes from torch's caching allocator, so the library allocates nothing
+        ws_bytes = _lib.lib().afa_fwd_workspace_size(dt, B, H, L, D, int(c is not None))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
         rc = _lib.lib().afa_fwd(
             dt, B, H, L, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _strides(q, k, v, out),
             _lib.ptr(out), _lib.ptr(den), _lib.ptr(c), _lib.ptr(s), rot_len, float(sink_omega),
             int(bool(causal)), 0 if valid_seq_len is None else int(valid_seq_len), flags,
-            _lib.stream_ptr(dev))
+            _lib.ptr(ws), ws_bytes, _lib.stream_ptr(dev))
     _lib.check(rc, "afa_fwd")
     return out, den
 
@@ -198,7 +202,7 @@ def tiled_afa_backward(
     d_total = d_total.to(_lib.accum_dtype(q.dtype)).contiguous()
     dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
     c, s, rot_len = _rotary_tables(rotary_params, q)
-    ws_bytes = _lib.lib().afa_bwd_workspace_size(dt, B, H, L, D)
+    ws_bytes = _lib.lib().afa_bwd_workspace_size(dt, B, H, L, D, int(c is not None))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         rc = _lib.lib().afa_bwd(

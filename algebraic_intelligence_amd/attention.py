@@ -232,9 +232,8 @@ def rotate_tensor(x: torch.Tensor, c: torch.Tensor, s: torch.Tensor, seq_axis: i
     (src/attention.py:142-152); c and s are (>= L, D/2) tables."""
     if x.shape[-1] % 2 != 0:
         raise ValueError(f"Feature dimension must be even, got {x.shape[-1]}")
-    pairs = x.shape[-1] // 2
-    c = c.reshape(-1, pairs)
-    s = s.reshape(-1, pairs)
+    c = _lib.table_2d(c, x.shape[-1])
+    s = _lib.table_2d(s, x.shape[-1])
     if c.shape[0] < x.shape[seq_axis]:
         raise ValueError("rotary tables are shorter than the sequence")
     return _Rotate.apply(_float_input(x), c, s, seq_axis % x.ndim)

@@ -37,36 +37,41 @@ int cu_count() {
   return cus[dev];
 }
 
-// Stream-ordered scratch from the current device's default memory pool.  The pool's release
-// threshold is raised once per device so that memory freed by one call is reused by the next
-// instead of being unmapped at every synchronisation.  Returns nullptr on failure.
+// Stream-ordered scratch for calls that pass no workspace, from a memory pool of this library
+// (one per device, created on first use; its release threshold keeps memory freed by one call for
+// the next instead of unmapping it at every synchronisation).  The device's default pool and
+// every other pool of the process keep their own settings.  Returns nullptr on failure.
 void* scratch_alloc(size_t bytes, hipStream_t s) {
   static std::once_flag once[64];
+  static hipMemPool_t pools[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   std::call_once(once[dev], [dev]() {
-    hipMemPool_t pool;
-    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+    hipMemPoolProps props = {};
+    props.allocType = hipMemAllocationTypePinned;
+    props.handleTypes = hipMemHandleTypeNone;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t pool = nullptr;
+    if (hipMemPoolCreate(&pool, &props) == hipSuccess) {
       uint64_t keep = UINT64_MAX;
       (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+      pools[dev] = pool;
+    } else {
+      (void)hipGetLastError();
+      pools[dev] = nullptr;
     }
   });
+  if (pools[dev] == nullptr) return nullptr;
   void* p = nullptr;
-  if (hipMallocAsync(&p, bytes, s) != hipSuccess) {
+  if (hipMallocFromPoolAsync(&p, bytes, pools[dev], s) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
   return p;
 }
 
-// The branch-free rho^8 for s < 0 carries, beyond a relative error of 32 * 2^-24, an absolute
-// cancellation error below 1e-8 per weight (a float32 sweep of s in [-1e4, 0] with the
-// hardware rsqrt off by up to one ulp gives 9.3e-9).  Over n keys that adds at most
-// n * 1e-8 / sink_omega to the relative error of out, and the fast form is used only where
-// this stays below 1e-3 (the bf16 rounding of P alone is 2e-3); never for fp32/fp64 inputs.
-bool fast_rho_ok(double sink_omega, int64_t seq_len) {
-  return sink_omega > 0.0 && (double)seq_len * 1e-8 / sink_omega < 1e-3;
-}
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct Strides {
   int64_t v[12];
@@ -120,159 +125,236 @@ int afa_last_hip_error(void) { return g_last_hip_error; }
 
 int afa_version(void) { return 1; }
 
-int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
-            const void* q, const void* k, const void* v, const int64_t* strides, void* out,
-            void* denom, const void* rot_cos, const void* rot_sin, int64_t rot_len,
-            double sink_omega, int causal, int64_t valid_len, unsigned flags, void* stream) {
-  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
-  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return AFA_ERR_NULL;
-  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return AFA_ERR_SHAPE;
-  if (batch * heads > INT32_MAX / 4 || seq_len > (INT32_MAX >> 2)) return AFA_ERR_SHAPE;
-  if (head_dim > 128 && head_dim % 128 != 0) return AFA_ERR_HEAD_DIM;
-  if (!finite_nonneg(sink_omega)) return AFA_ERR_SINK;
-  if (valid_len < 0 || valid_len > seq_len) return AFA_ERR_VALID_LEN;
-  int rc = check_rotary(rot_cos, rot_sin, rot_len, seq_len, head_dim);
-  if (rc != AFA_OK) return rc;
-  const int vlen = valid_len == 0 ? (int)seq_len : (int)valid_len;
-  const Strides st = resolve_strides(strides, heads, seq_len, head_dim);
-  hipStream_t s = (hipStream_t)stream;
+}  // extern "C"
 
-  // bf16/fp16 matrix-core kernels: the fully fused one (afa_fwd_mfma.hip, head_dim 64 and 128)
-  // and the pipelined ones (head_dim 32, 48, 64, 96, 128)
-  const bool fused_ok = afa::mfma_fwd_supported(dtype, (int)head_dim);
-  // the pipelined kernels address K and V rows by 32-bit byte offsets from the head's base
-  auto in_head_32 = [&](int64_t row_stride) {
-    return row_stride >= 0 && (seq_len - 1) * row_stride + head_dim < (int64_t(1) << 31);
-  };
-  const bool pipe_ok = afa::pipe_fwd_supported(dtype, (int)head_dim) && in_head_32(st.v[5]) &&
-                       in_head_32(st.v[8]);
-  bool use_mfma = (fused_ok || pipe_ok) && !(flags & AFA_FLAG_GENERIC) && !(flags & AFA_FLAG_EXACT_REF);
-  if (use_mfma) {
-    // 16-byte vector loads/stores: 8-element aligned row strides and 16-byte aligned bases.
-    for (int i = 0; i < 12; ++i)
-      if (st.v[i] % 8 != 0) use_mfma = false;
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) use_mfma = false;
-    if (rot_cos != nullptr && (!aligned16(rot_cos) || !aligned16(rot_sin))) use_mfma = false;
-  }
-  if (use_mfma) {
-    afa::FwdArgs a = {};
-    a.q = q; a.k = k; a.v = v; a.out = out; a.denom = (float*)denom;
-    a.rc = (const float*)rot_cos; a.rs = (const float*)rot_sin;
-    a.q_b = st.v[0]; a.q_h = st.v[1]; a.q_l = st.v[2];
-    a.k_b = st.v[3]; a.k_h = st.v[4]; a.k_l = st.v[5];
-    a.v_b = st.v[6]; a.v_h = st.v[7]; a.v_l = st.v[8];
-    a.o_b = st.v[9]; a.o_h = st.v[10]; a.o_l = st.v[11];
-    a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len;
-    a.valid_len = vlen;
-    a.causal = causal ? 1 : 0;
-    a.omega = (float)sink_omega;
-    a.q_scale = 1.0f;
-    a.w_unscale = 1.0f;
-    a.s_mult = 1.0f;
-    const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, vlen);
-    // AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel where it exists
+namespace {
+
+// ---------------------------------------------------------------------------------- forward
+// Path of an afa_fwd call and the workspace it needs (byte offsets of 256-byte aligned regions):
+//   bf16 / fp16 matrix-core kernels: the fast-rho guard's key bounds (B H ceil(L/64) floats),
+//     then, with rotary tables on the pipelined kernels, the rotated k (B H L D elements);
+//   fp32 matrix-core kernel: the split-K partials when its grid is split;
+//   generic kernel: nothing.
+enum { FWD_GENERIC = 0, FWD_FUSED = 1, FWD_PIPE = 2, FWD_F32 = 3 };
+struct FwdPlan {
+  int kind = FWD_GENERIC;
+  bool wide = false;  // FWD_PIPE at head_dim 64: the 256-query kernel (afa_fwd_d64.hip)
+  bool rotk = false;  // FWD_PIPE with rotary tables: k rotated once into the workspace
+  int nsplit = 1;     // FWD_F32: key splits
+  size_t kbm = 0, krot = 0, part = 0, total = 0;
+};
+
+// mfma_layout: 16-byte aligned q, k, v, out (and tables) with 8-element strides; f32_layout: the
+// fp32 kernel's float4 rows of v and out; in_head_32: K and V rows addressable by 32-bit byte
+// offsets within a head (the pipelined kernels' loads).
+FwdPlan fwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, int64_t vlen, bool rotary,
+                 bool mfma_layout, bool f32_layout, bool in_head_32, unsigned flags) {
+  FwdPlan p;
+  if (flags & (AFA_FLAG_GENERIC | AFA_FLAG_EXACT_REF)) return p;
+  const bool fused_ok = afa::mfma_fwd_supported(dtype, (int)D);
+  const bool pipe_ok = afa::pipe_fwd_supported(dtype, (int)D) && in_head_32;
+  if ((fused_ok || pipe_ok) && mfma_layout) {
+    size_t off = align256((size_t)(B * H * ((L + 63) / 64)) * sizeof(float));
     if (pipe_ok && !(fused_ok && (flags & AFA_FLAG_SIMPLE_SCHEDULE))) {
-      afa::FwdArgs b = a;
+      p.kind = FWD_PIPE;
       // head_dim 64: 256-query workgroups at two per CU (afa_fwd_d64.hip) when they fill at least
       // one and a half rounds of those slots; otherwise, and at the other head dims, 128-query
       // workgroups with several waves per SIMD (afa_fwd_pipe.hip).  With a single round (C4: 512
       // workgroups on 256 CUs) the finer causal blocks of the 128-query kernel balance better:
       // 0.0545 against 0.0560 ms, measured on one box.
-      const int64_t nwg256 = (int64_t)b.B * b.H * ((seq_len + 255) / 256);
-      const bool wide = head_dim == 64 && nwg256 >= 3 * (int64_t)cu_count();
-      // with rotary tables k is rotated once into stream-ordered scratch; without that scratch
-      // the fully fused kernel below (head_dim 64, 128) or the generic one rotates at tile load
-      void* krot = nullptr;
-      if (rot_cos != nullptr) krot = scratch_alloc(afa::krot_bytes(b, (int)head_dim), s);
-      if (rot_cos == nullptr || krot != nullptr) {
-        hipError_t e = krot != nullptr ? afa::krot_launch(dtype, (int)head_dim, b, krot, s) : hipSuccess;
-        if (e == hipSuccess) {
-          if (wide) {
-            b.nqb = (int)((seq_len + 255) / 256);
-            e = afa::d64_fwd_launch(dtype, b, exact, s);
-          } else {
-            e = afa::pipe_fwd_launch(dtype, (int)head_dim, b, exact, s);
-          }
-        }
-        if (krot != nullptr) {
-          hipError_t e2 = hipFreeAsync(krot, s);
-          if (e == hipSuccess) e = e2;
-        }
-        return hip_status(e);
+      p.wide = D == 64 && B * H * ((L + 255) / 256) >= 3 * (int64_t)cu_count();
+      if (rotary) {
+        p.rotk = true;
+        p.krot = off;
+        off += align256((size_t)(B * H * L * D) * 2);
       }
+    } else {
+      p.kind = FWD_FUSED;
     }
-    if (fused_ok) {
-      const int qpb = afa::mfma_fwd_queries_per_block((int)head_dim);
-      a.nqb = (int)((seq_len + qpb - 1) / qpb);
-      return hip_status(afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s));
-    }
+    p.total = off;
+    return p;
   }
-  if (dtype == AFA_F32 && afa::f32_fwd_supported((int)head_dim) &&
-      !(flags & (AFA_FLAG_GENERIC | AFA_FLAG_EXACT_REF))) {
-    // float4 rows of v and out
-    bool ok = aligned16(v) && aligned16(out);
-    for (int i : {6, 7, 8, 9, 10, 11})
-      if (st.v[i] % 4 != 0) ok = false;
-    if (ok) {
-      afa::FwdArgs a = {};
-      a.q = q; a.k = k; a.v = v; a.out = out; a.denom = (float*)denom;
-      a.rc = (const float*)rot_cos; a.rs = (const float*)rot_sin;
-      a.q_b = st.v[0]; a.q_h = st.v[1]; a.q_l = st.v[2];
-      a.k_b = st.v[3]; a.k_h = st.v[4]; a.k_l = st.v[5];
-      a.v_b = st.v[6]; a.v_h = st.v[7]; a.v_l = st.v[8];
-      a.o_b = st.v[9]; a.o_h = st.v[10]; a.o_l = st.v[11];
-      a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len;
-      a.valid_len = vlen;
-      a.causal = causal ? 1 : 0;
-      a.q_scale = (float)(1.0 / std::sqrt((double)head_dim));
-      a.omega = (float)sink_omega;
-      a.w_unscale = 1.0f;
-      // fewer 128-query workgroups than CUs: split every query block's key tiles over up to
-      // 2 * CUs workgroups in all (partials in stream-ordered scratch, then a combine kernel)
-      const int64_t nwg = batch * heads * ((seq_len + 127) / 128);
-      const int64_t key_tiles = (vlen + 31) / 32;
-      const int64_t cus = cu_count();
-      int nsplit = 1;
-      if (nwg < cus && key_tiles > 1) nsplit = (int)std::min<int64_t>(key_tiles, (2 * cus + nwg - 1) / nwg);
-      void* part = nullptr;
-      if (nsplit > 1) {
-        part = scratch_alloc(afa::f32_fwd_part_floats(a, (int)head_dim, nsplit) * sizeof(float), s);
-        if (part == nullptr) nsplit = 1;
-      }
-      a.part = (float*)part;
-      hipError_t e = afa::f32_fwd_launch((int)head_dim, a, nsplit, s);
-      if (part != nullptr) {
-        hipError_t e2 = hipFreeAsync(part, s);
-        if (e == hipSuccess) e = e2;
-      }
-      return hip_status(e);
-    }
+  if (dtype == AFA_F32 && afa::f32_fwd_supported((int)D) && f32_layout) {
+    p.kind = FWD_F32;
+    // fewer 128-query workgroups than CUs: split every query block's key tiles over up to
+    // 2 * CUs workgroups in all (partials in the workspace, then a combine kernel)
+    const int64_t nwg = B * H * ((L + 127) / 128);
+    const int64_t key_tiles = (vlen + 31) / 32;
+    const int64_t cus = cu_count();
+    if (nwg < cus && key_tiles > 1) p.nsplit = (int)std::min<int64_t>(key_tiles, (2 * cus + nwg - 1) / nwg);
+    if (p.nsplit > 1) p.total = align256((size_t)p.nsplit * B * H * L * (D + 1) * sizeof(float));
   }
-  if (head_dim > 256) return AFA_ERR_UNSUPPORTED;
-  afa::GenArgs g = {};
-  g.q = q; g.k = k; g.v = v; g.out = out; g.denom = denom;
-  g.rc = rot_cos; g.rs = rot_sin;
-  g.q_b = st.v[0]; g.q_h = st.v[1]; g.q_l = st.v[2];
-  g.k_b = st.v[3]; g.k_h = st.v[4]; g.k_l = st.v[5];
-  g.v_b = st.v[6]; g.v_h = st.v[7]; g.v_l = st.v[8];
-  g.o_b = st.v[9]; g.o_h = st.v[10]; g.o_l = st.v[11];
-  g.B = (int)batch; g.H = (int)heads; g.L = (int)seq_len; g.D = (int)head_dim;
-  g.valid_len = vlen;
-  g.causal = causal ? 1 : 0;
-  g.exact_ref = (flags & AFA_FLAG_EXACT_REF) ? 1 : 0;
-  g.scale = 1.0 / std::sqrt((double)head_dim);
-  if (dtype != AFA_F64) g.scale = (double)(float)g.scale;
-  g.omega = dtype == AFA_F64 ? sink_omega : (double)(float)sink_omega;
-  return hip_status(afa::generic_fwd_launch(dtype, g, s));
+  return p;
 }
 
-size_t afa_bwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t seq_len,
-                              int64_t head_dim) {
-  (void)head_dim;
-  if (!valid_dtype(dtype) || batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+int fwd_check(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return AFA_ERR_SHAPE;
+  if (batch * heads > INT32_MAX / 4 || seq_len > (INT32_MAX >> 2)) return AFA_ERR_SHAPE;
+  if (head_dim > 128 && head_dim % 128 != 0) return AFA_ERR_HEAD_DIM;
+  return AFA_OK;
+}
+
+// ---------------------------------------------------------------------------------- backward
+// Workspace of afa_bwd (256-byte aligned regions): E and 1/d per row (every path); on the
+// bf16 / fp16 matrix-core path the fast-rho guard's q and k bounds (2 B H ceil(L/64) floats) and,
+// with rotary tables, the rotated q and k (2 B H L D elements).
+struct BwdPlan {
+  bool mfma16 = false;
+  size_t e = 0, qbm = 0, kbm = 0, rot = 0, total = 0;
+};
+
+BwdPlan bwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, bool rotary, bool mfma_ok) {
+  BwdPlan p;
   // E and 1/d per row; each head's rows padded to a multiple of 4 (the matrix-core kernels load
   // them in 16-byte chunks)
-  return (size_t)(batch * heads * ((seq_len + 3) / 4 * 4)) * acc_size(dtype) * 2;
+  size_t off = align256((size_t)(B * H * ((L + 3) / 4 * 4)) * acc_size(dtype) * 2);
+  if (mfma_ok) {
+    p.mfma16 = true;
+    const size_t nb = align256((size_t)(B * H * ((L + 63) / 64)) * sizeof(float));
+    p.qbm = off;
+    p.kbm = off + nb;
+    off += 2 * nb;
+    if (rotary) {
+      p.rot = off;
+      off += align256((size_t)(B * H * L * D) * 2 * 2);
+    }
+  }
+  p.total = off;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t afa_fwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                              int rotary) {
+  if (fwd_check(dtype, batch, heads, seq_len, head_dim) != AFA_OK) return 0;
+  const bool in_head = (seq_len - 1) * head_dim + head_dim < (int64_t(1) << 31);
+  return fwd_plan(dtype, batch, heads, seq_len, head_dim, seq_len, rotary != 0, true, true, in_head, 0).total;
+}
+
+int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+            const void* q, const void* k, const void* v, const int64_t* strides, void* out,
+            void* denom, const void* rot_cos, const void* rot_sin, int64_t rot_len,
+            double sink_omega, int causal, int64_t valid_len, unsigned flags, void* workspace,
+            size_t workspace_bytes, void* stream) {
+  int rc = fwd_check(dtype, batch, heads, seq_len, head_dim);
+  if (rc != AFA_OK) return rc;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return AFA_ERR_NULL;
+  if (!finite_nonneg(sink_omega)) return AFA_ERR_SINK;
+  if (valid_len < 0 || valid_len > seq_len) return AFA_ERR_VALID_LEN;
+  rc = check_rotary(rot_cos, rot_sin, rot_len, seq_len, head_dim);
+  if (rc != AFA_OK) return rc;
+  const int vlen = valid_len == 0 ? (int)seq_len : (int)valid_len;
+  const Strides st = resolve_strides(strides, heads, seq_len, head_dim);
+  hipStream_t s = (hipStream_t)stream;
+
+  // 16-byte vector loads/stores: 8-element aligned strides and 16-byte aligned bases
+  bool mfma_layout = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
+                     (rot_cos == nullptr || (aligned16(rot_cos) && aligned16(rot_sin)));
+  for (int i = 0; i < 12; ++i)
+    if (st.v[i] % 8 != 0) mfma_layout = false;
+  bool f32_layout = aligned16(v) && aligned16(out);
+  for (int i : {6, 7, 8, 9, 10, 11})
+    if (st.v[i] % 4 != 0) f32_layout = false;
+  auto in_head_32 = [&](int64_t row_stride) {
+    return row_stride >= 0 && (seq_len - 1) * row_stride + head_dim < (int64_t(1) << 31);
+  };
+  const FwdPlan plan = fwd_plan(dtype, batch, heads, seq_len, head_dim, vlen, rot_cos != nullptr, mfma_layout,
+                                f32_layout, in_head_32(st.v[5]) && in_head_32(st.v[8]), flags);
+
+  char* ws = (char*)workspace;
+  bool owned = false;
+  if (plan.total > 0) {
+    if (ws == nullptr) {
+      ws = (char*)scratch_alloc(plan.total, s);
+      if (ws == nullptr) return hip_status(hipErrorOutOfMemory);
+      owned = true;
+    } else if (workspace_bytes < plan.total) {
+      return AFA_ERR_WORKSPACE;
+    } else if (!aligned16(ws)) {
+      return AFA_ERR_ALIGN;
+    }
+  }
+
+  afa::FwdArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.out = out; a.denom = (float*)denom;
+  a.rc = (const float*)rot_cos; a.rs = (const float*)rot_sin;
+  a.q_b = st.v[0]; a.q_h = st.v[1]; a.q_l = st.v[2];
+  a.k_b = st.v[3]; a.k_h = st.v[4]; a.k_l = st.v[5];
+  a.v_b = st.v[6]; a.v_h = st.v[7]; a.v_l = st.v[8];
+  a.o_b = st.v[9]; a.o_h = st.v[10]; a.o_l = st.v[11];
+  a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len;
+  a.valid_len = vlen;
+  a.causal = causal ? 1 : 0;
+  a.omega = (float)sink_omega;
+  a.q_scale = 1.0f;
+  a.w_unscale = 1.0f;
+  a.s_mult = 1.0f;
+  // the branch-free rho^8 runs only on tiles the fast-rho guard clears, unless the caller asks
+  // for the two-branch form everywhere
+  const bool exact = (flags & AFA_FLAG_EXACT_TAIL) != 0;
+  hipError_t e = hipSuccess;
+  if (plan.kind == FWD_PIPE || plan.kind == FWD_FUSED) {
+    float* kbm = (float*)(ws + plan.kbm);
+    if (plan.rotk) {
+      e = afa::krot_launch(dtype, (int)head_dim, a, ws + plan.krot, kbm, s);  // a.k, a.kbm now the rotated k
+    } else if (!exact) {
+      e = afa::rownorm_launch(dtype, k, st.v[3], st.v[4], st.v[5], a.B, a.H, a.L, (int)head_dim, kbm, s);
+      a.kbm = kbm;
+      a.nkb = (a.L + 63) / 64;
+    }
+    if (e == hipSuccess) {
+      if (plan.kind == FWD_FUSED) {
+        a.nqb = (int)((seq_len + afa::mfma_fwd_queries_per_block((int)head_dim) - 1) /
+                      afa::mfma_fwd_queries_per_block((int)head_dim));
+        e = afa::mfma_fwd_launch(dtype, (int)head_dim, a, exact, s);
+      } else if (plan.wide) {
+        a.nqb = (int)((seq_len + 255) / 256);
+        e = afa::d64_fwd_launch(dtype, a, exact, s);
+      } else {
+        e = afa::pipe_fwd_launch(dtype, (int)head_dim, a, exact, s);
+      }
+    }
+  } else if (plan.kind == FWD_F32) {
+    a.q_scale = (float)(1.0 / std::sqrt((double)head_dim));
+    a.part = plan.nsplit > 1 ? (float*)(ws + plan.part) : nullptr;
+    e = afa::f32_fwd_launch((int)head_dim, a, plan.nsplit, s);
+  } else {
+    if (head_dim > 256) {
+      if (owned) (void)hipFreeAsync(ws, s);
+      return AFA_ERR_UNSUPPORTED;
+    }
+    afa::GenArgs g = {};
+    g.q = q; g.k = k; g.v = v; g.out = out; g.denom = denom;
+    g.rc = rot_cos; g.rs = rot_sin;
+    g.q_b = st.v[0]; g.q_h = st.v[1]; g.q_l = st.v[2];
+    g.k_b = st.v[3]; g.k_h = st.v[4]; g.k_l = st.v[5];
+    g.v_b = st.v[6]; g.v_h = st.v[7]; g.v_l = st.v[8];
+    g.o_b = st.v[9]; g.o_h = st.v[10]; g.o_l = st.v[11];
+    g.B = (int)batch; g.H = (int)heads; g.L = (int)seq_len; g.D = (int)head_dim;
+    g.valid_len = vlen;
+    g.causal = causal ? 1 : 0;
+    g.exact_ref = (flags & AFA_FLAG_EXACT_REF) ? 1 : 0;
+    g.scale = 1.0 / std::sqrt((double)head_dim);
+    if (dtype != AFA_F64) g.scale = (double)(float)g.scale;
+    g.omega = dtype == AFA_F64 ? sink_omega : (double)(float)sink_omega;
+    e = afa::generic_fwd_launch(dtype, g, s);
+  }
+  if (owned) {
+    hipError_t e2 = hipFreeAsync(ws, s);
+    if (e == hipSuccess) e = e2;
+  }
+  return hip_status(e);
+}
+
+size_t afa_bwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                              int rotary) {
+  if (!valid_dtype(dtype) || batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return 0;
+  return bwd_plan(dtype, batch, heads, seq_len, head_dim, rotary != 0,
+                  afa::mfma_bwd_supported(dtype, (int)head_dim, seq_len)).total;
 }
 
 int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
@@ -292,19 +374,28 @@ int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   int rc = check_rotary(rot_cos, rot_sin, rot_len, seq_len, head_dim);
   if (rc != AFA_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const size_t need = afa_bwd_workspace_size(dtype, batch, heads, seq_len, head_dim);
-  void* ws = workspace;
+  const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(g) &&
+                       aligned16(dq) && aligned16(dk) && aligned16(dv) && aligned16(denom) &&
+                       (workspace == nullptr || aligned16(workspace));
+  const bool use_mfma = !(flags & AFA_FLAG_GENERIC) && aligned &&
+                        afa::mfma_bwd_supported(dtype, (int)head_dim, seq_len) &&
+                        (rot_cos == nullptr || (aligned16(rot_cos) && aligned16(rot_sin)));
+  // fp32: the fp32 matrix-core kernels (q and k rotated as they are staged)
+  const bool use_f32 = dtype == AFA_F32 && !(flags & AFA_FLAG_GENERIC) && aligned &&
+                       afa::f32_bwd_supported((int)head_dim);
+  const BwdPlan plan = bwd_plan(dtype, batch, heads, seq_len, head_dim, rot_cos != nullptr, use_mfma);
+  char* ws = (char*)workspace;
   bool owned = false;
   if (ws == nullptr) {
-    hipError_t e = hipMallocAsync(&ws, need, s);
-    if (e != hipSuccess) return hip_status(e);
+    ws = (char*)scratch_alloc(plan.total, s);
+    if (ws == nullptr) return hip_status(hipErrorOutOfMemory);
     owned = true;
-  } else if (workspace_bytes < need) {
+  } else if (workspace_bytes < plan.total) {
     return AFA_ERR_WORKSPACE;
   }
   afa::GenArgs a = {};
   a.q = q; a.k = k; a.v = v; a.out_in = out; a.dtot = denom; a.g = g;
-  a.out = dq; a.dk = dk; a.dv = dv; a.e_ws = ws;
+  a.out = dq; a.dk = dk; a.dv = dv; a.e_ws = ws + plan.e;
   a.rc = rot_cos; a.rs = rot_sin;
   a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len; a.D = (int)head_dim;
   a.valid_len = valid_len == 0 ? (int)seq_len : (int)valid_len;
@@ -312,26 +403,14 @@ int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   a.scale = 1.0 / std::sqrt((double)head_dim);
   if (dtype != AFA_F64) a.scale = (double)(float)a.scale;
   a.omega = sink_omega;
-  const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(g) &&
-                       aligned16(dq) && aligned16(dk) && aligned16(dv) && aligned16(ws) && aligned16(denom);
-  bool use_mfma = !(flags & AFA_FLAG_GENERIC) && aligned && afa::mfma_bwd_supported(dtype, (int)head_dim, seq_len) &&
-                  (rot_cos == nullptr || (aligned16(rot_cos) && aligned16(rot_sin)));
-  // rotary tables: q and k are rotated once into stream-ordered scratch (else the generic kernel)
-  void* rot = nullptr;
-  if (use_mfma && rot_cos != nullptr) {
-    rot = scratch_alloc(afa::mfma_bwd_rot_bytes(a), s);
-    if (rot == nullptr) use_mfma = false;
-  }
-  const bool exact = (flags & AFA_FLAG_EXACT_TAIL) || !fast_rho_ok(sink_omega, a.valid_len);
-  // fp32: the fp32 matrix-core kernels (q and k rotated as they are staged)
-  const bool use_f32 = dtype == AFA_F32 && !(flags & AFA_FLAG_GENERIC) && aligned &&
-                       afa::f32_bwd_supported((int)head_dim);
-  hipError_t e = use_mfma  ? afa::mfma_bwd_launch(dtype, a, exact, rot, s)
-                 : use_f32 ? afa::f32_bwd_launch(a, s)
-                           : afa::generic_bwd_launch(dtype, a, s);
-  if (rot != nullptr) {
-    hipError_t e2 = hipFreeAsync(rot, s);
-    if (e == hipSuccess) e = e2;
+  const bool exact = (flags & AFA_FLAG_EXACT_TAIL) != 0;
+  hipError_t e;
+  if (use_mfma) {
+    a.qbm = (const float*)(ws + plan.qbm);
+    a.kbm = (const float*)(ws + plan.kbm);
+    e = afa::mfma_bwd_launch(dtype, a, exact, rot_cos != nullptr ? ws + plan.rot : nullptr, s);
+  } else {
+    e = use_f32 ? afa::f32_bwd_launch(a, s) : afa::generic_bwd_launch(dtype, a, s);
   }
   if (owned) {
     hipError_t e2 = hipFreeAsync(ws, s);

@@ -105,10 +105,14 @@ __device__ __forceinline__ float rho8_exact(float s) {
 }
 
 // Branch-free evaluation rho = s + sqrt(1 + s^2) computed as fma(t, rsqrt(t), s) for both
-// signs.  Exact for s >= 0 (same expression as the reference's positive branch); for s < 0
-// the cancellation adds an absolute error below 1e-8 to rho^8 (about 8 rho(s)^7 |s| 2^-22),
-// which the host accepts only when sink_omega makes it negligible against the denominator
-// (fast_rho_ok in afa_capi.hip).
+// signs.  Exact for s >= 0 (same expression as the reference's positive branch).  For s < 0
+// the sum cancels: t r = sqrt(1 + s^2) (1 + eta) with eta <= 2^-25 + 1.5 * 2^-23 (the rounding
+// of t, halved by the square root, and the hardware rsqrt's rounding and one ulp), so
+// fma(t, r, s) carries an absolute error of about |s| eta against rho(s) ~ 1/(2|s|), a relative
+// error of 16 s^2 eta in rho^8.  The kernels therefore use this form only in waves whose every
+// score is provably within |s| <= kFastRhoMaxScore (fast_rho_safe below), where that is at most
+// 16 * 32^2 * 2.1e-7 = 3.4e-3 per weight; other waves, and every wave when the caller sets
+// AFA_FLAG_EXACT_TAIL, take rho8_exact.
 __device__ __forceinline__ float rho8_fast(float s) {
   const float t = __builtin_fmaf(s, s, 1.0f);
   const float r = __builtin_amdgcn_rsqf(t);
@@ -129,6 +133,68 @@ __device__ __forceinline__ float rho8_fast_half(float x) {
   const float p2 = rho * rho;
   const float p4 = p2 * p2;
   return p4 * p4;
+}
+
+// Two-branch form of rho8_fast_half: (rho(s)/sqrt 2)^8 = rho(s)^8 / 16 for s = sqrt(2) x without
+// cancellation.  For s < 0, rho(s) = 1/rho(|s|), so (rho(s)/sqrt 2)^8 = 1 / (256 (rho(|s|)/sqrt 2)^8).
+__device__ __forceinline__ float rho8_exact_half(float x) {
+  const float a = __builtin_fabsf(x);
+  const float t = __builtin_fmaf(a, a, 0.5f);
+  const float r = __builtin_amdgcn_rsqf(t);
+  const float rho = __builtin_fmaf(t, r, a);
+  const float p2 = rho * rho;
+  const float p4 = p2 * p2;
+  const float p8 = p4 * p4;
+  const float inv = __builtin_amdgcn_rcpf(p8 * 256.0f);
+  return x < 0.0f ? inv : p8;
+}
+
+// ------------------------------------------------------------------ fast-rho guard
+// Largest |score| on which the branch-free rho^8 is used (see rho8_fast).
+constexpr float kFastRhoMaxScore = 32.0f;
+
+// Sum of squares of the 8 packed 16-bit elements of a 16-byte chunk, in fp32 (v_dot2).
+template <int DT>
+__device__ __forceinline__ float chunk_norm2(u32x4_t w) {
+  float s = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    if constexpr (DT == AFA_BF16) {
+      const bf16x2_t v = __builtin_bit_cast(bf16x2_t, w[p]);
+      s = __builtin_amdgcn_fdot2_f32_bf16(v, v, s, false);
+    } else {
+      const f16x2_t v = __builtin_bit_cast(f16x2_t, w[p]);
+      s = __builtin_amdgcn_fdot2(v, v, s, false);
+    }
+  }
+  return s;
+}
+
+// Maximum of a per-lane value over the wave, returned wave-uniform.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// Choice between rho8_fast and rho8_exact for one wave.  `nb2` holds, for each 64-row block of
+// the other operand's head, the largest squared row norm (afa_rownorm_kernel / the rotation
+// pre-passes); `vmax2` is the largest squared row norm of this wave's own operand rows as the
+// MFMA sees them.  By Cauchy-Schwarz every score formed from block j satisfies
+// s^2 <= score_scale^2 * vmax2 * nb2[j], and `lim` is kFastRhoMaxScore^2 / score_scale^2 less a
+// margin for rounding (set by the host).  Returns true, wave-uniform, when every block in
+// [blk0, blk1) satisfies vmax2 * nb2[j] <= lim (one ballot per 64 blocks; NaN compares false, and
+// such waves take the exact form, which propagates the NaN as the reference does);
+// nb2 == nullptr gives false.
+__device__ __forceinline__ bool fast_rho_safe(const float* nb2, int blk0, int blk1, float vmax2, float lim) {
+  if (nb2 == nullptr) return false;
+  bool ok = true;
+  for (int base = blk0; base < blk1; base += 64) {
+    const int j = base + (int)(threadIdx.x & 63);
+    const float m = j < blk1 ? nb2[j] : 0.0f;
+    ok = ok && __ballot(!(m * vmax2 <= lim)) == 0;
+  }
+  return ok;
 }
 
 // Reference-faithful double precision evaluation (two branches, IEEE sqrt and division).

@@ -82,6 +82,11 @@ __device__ __forceinline__ float tree16(const float (&p)[16]) {
 }  // namespace
 
 
+// LDS tiles of the head_dim-64 kernel: a ring of D64_NB tiles of D64_KT keys x 64 features.
+constexpr int D64_KT = 64;
+constexpr int D64_NB = 4;
+typedef unsigned short D64Tile[D64_KT * 64];
+
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9: vmcnt [3:0] and [15:14]; expcnt and
 // lgkmcnt at their no-wait maxima).
 __host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
@@ -89,14 +94,19 @@ __host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 
 // Cayley rotation of K, once per call: y (contiguous B, H, L, D) = rotate(x) in fp32 with the
 // (L, D/2) fp32 tables, rounded once to the element type -- the values the fused loaders would
 // produce (rot4 with scale 1).  Grid (ceil(L / 64), B * H); a block rotates 64 key rows, thread
-// slot e = tid + 256 i covering row e / (D/8), 16-byte chunk e % (D/8).
+// slot e = tid + 256 i covering row e / (D/8), 16-byte chunk e % (D/8).  It also writes the
+// largest squared norm of the block's rotated rows (as rounded) to nb2[bh * gridDim.x + block],
+// the key bound of the fast-rho guard.
 template <int DT, int D>
-__global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y) {
+__global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y, float* nb2) {
   constexpr int CH = D / 8;
+  __shared__ float rn[64];
   const int bh = blockIdx.y;
   const int b = bh / a.H, h = bh % a.H;
   const unsigned short* xb = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   unsigned short* yb = y + (int64_t)bh * a.L * D;
+  if (threadIdx.x < 64) rn[threadIdx.x] = 0.0f;
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < (64 * CH + 255) / 256; ++i) {
     const int e = threadIdx.x + 256 * i;
@@ -105,24 +115,29 @@ __global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned
       const u32x4_t w = *(const u32x4_t*)(xb + (int64_t)l * a.k_l + ch * 8);
       const f32x4_t cc = *(const f32x4_t*)(a.rc + (int64_t)l * (D / 2) + ch * 4);
       const f32x4_t ss = *(const f32x4_t*)(a.rs + (int64_t)l * (D / 2) + ch * 4);
-      *(u32x4_t*)(yb + (int64_t)l * D + ch * 8) = rot4<DT>(w, cc, ss, 1.0f);
+      const u32x4_t r = rot4<DT>(w, cc, ss, 1.0f);
+      *(u32x4_t*)(yb + (int64_t)l * D + ch * 8) = r;
+      atomicAdd(&rn[e / CH], chunk_norm2<DT>(r));
     }
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const float m = wave_max(rn[threadIdx.x]);
+    if (threadIdx.x == 0) nb2[(int64_t)bh * gridDim.x + blockIdx.x] = m;
   }
 }
 
-template <int DT, bool EXACT, bool ROT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void afa_fwd_d64_kernel(const FwdArgs a) {
+// Tile loop and epilogue of afa_fwd_d64_kernel for one form of rho^8: FAST, the branch-free
+// rho8_fast (the wave's scores are all within the fast-rho bound), else the two-branch
+// rho8_exact.  The kernel instantiates both and each wave runs one, so the two loops get their
+// own register allocation; the barriers count waves, not code locations.
+template <int DT, bool FAST>
+__device__ __forceinline__ void d64_body(const FwdArgs& a, D64Tile* lds_k, D64Tile* lds_v, const u32x4_t (&qf)[2][4],
+                                         int bh, int qblk) {
   constexpr int D = 64;
-  constexpr int KT = 64;        // keys per LDS tile
-  constexpr int NB = 4;         // LDS tile buffers (a ring: tile t in buffer t & 3)
+  constexpr int KT = D64_KT;
+  constexpr int NB = D64_NB;
   constexpr int LOADS = 4;      // direct loads per thread per tile (2 K + 2 V chunks)
-  // K and V tiles are row-major, 128 B per key row, 16-byte chunks XOR-swizzled: K chunk
-  // c of row r sits at c ^ (r & 7) (conflict-free 32-row fragment reads), V chunk c at
-  // c ^ (((r >> 1) & 1) << 2) (conflict-free ds_read_tr16_b64 of 4-key column slices).
-  __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * D];
-  __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * D];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -130,9 +145,6 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   const int g = lane >> 5;
   const int l16 = lane & 15;
   const int m16 = (lane >> 4) & 1;
-
-  int bh, qblk;
-  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
   const int b = bh / a.H;
   const int h = bh % a.H;
   const int L = a.L;
@@ -145,32 +157,13 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   const int ntiles = (kend_wg + KT - 1) / KT;
   const int nsub = q0_w < L ? (kend_w + 31) / 32 : 0;  // 32-key sub-tiles of this wave
   const int U = 2 * nsub;                                // units of this wave
-  const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
   const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
-
-  // ---- Q fragments: query q0_w + qb*32 + l32, features kc*16 + 8g .. +7 (scaled, rotated)
-  u32x4_t qf[2][4];
+  // rho^8 of one unit's 16 scores per lane
+  auto rho8_unit = [&](float (&p)[16], const f32x16_t& sv) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qi = q0_w + qb * 32 + l32;
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      const int d0 = kc * 16 + 8 * g;
-      u32x4_t w = {0u, 0u, 0u, 0u};
-      if (qi < L) {
-        w = *(const u32x4_t*)(qp + (int64_t)qi * a.q_l + d0);
-        if constexpr (ROT) {
-          const f32x4_t c = *(const f32x4_t*)(a.rc + (int64_t)qi * (D / 2) + d0 / 2);
-          const f32x4_t s = *(const f32x4_t*)(a.rs + (int64_t)qi * (D / 2) + d0 / 2);
-          w = rot4<DT>(w, c, s, a.q_scale);
-        } else {
-          w = scl4<DT>(w, a.q_scale);
-        }
-      }
-      qf[qb][kc] = w;
-    }
-  }
+    for (int r = 0; r < 16; ++r) p[r] = FAST ? rho8_fast(sv[r]) : rho8_exact(sv[r]);
+  };
 
   // ---- tile staging by direct global -> LDS loads.  Thread chunk c = tid + 256 i covers key
   // row c >> 3 of the tile and physical 16-byte column c & 7; it loads the logical chunk that
@@ -293,8 +286,7 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) sA = mma<DT>(kf[kc], qf[1][kc], sA);
     float p[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = EXACT ? rho8_exact(s0[r]) : rho8_fast(s0[r]);
+    rho8_unit(p, s0);
     mask16(p, 0);
     finish_p(p, 0);
     read_kf(1, kf);
@@ -321,8 +313,7 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
       for (int db = 0; db < 2; ++db) o[db][PQ] = mma<DT>(vf[db][kk], p_prev[kk], o[db][PQ]);
     if (u < U) {
       float p[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = EXACT ? rho8_exact(scur[r]) : rho8_fast(scur[r]);
+      rho8_unit(p, scur);
       mask16(p, u);
       finish_p(p, QB);
       if constexpr (QB == 0) {
@@ -371,6 +362,75 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
 }
 
 template <int DT, bool EXACT, bool ROT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void afa_fwd_d64_kernel(const FwdArgs a) {
+  constexpr int D = 64;
+  // K and V tiles are row-major, 128 B per key row, 16-byte chunks XOR-swizzled: K chunk
+  // c of row r sits at c ^ (r & 7) (conflict-free 32-row fragment reads), V chunk c at
+  // c ^ (((r >> 1) & 1) << 2) (conflict-free ds_read_tr16_b64 of 4-key column slices).
+  __shared__ __attribute__((aligned(16))) D64Tile lds_k[D64_NB];
+  __shared__ __attribute__((aligned(16))) D64Tile lds_v[D64_NB];
+
+  int bh, qblk;
+  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  const int b = bh / a.H;
+  const int h = bh % a.H;
+  const int L = a.L;
+  const int vlen = a.valid_len;
+
+  const int q0_wg = qblk * 256;
+  const int q0_w = q0_wg + wave * 64;
+  const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 256)) : vlen;
+  const int kend_w = a.causal ? min(vlen, q0_w + 64) : vlen;
+  const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
+
+  // ---- Q fragments: query q0_w + qb*32 + l32, features kc*16 + 8g .. +7 (scaled, rotated)
+  u32x4_t qf[2][4];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qi = q0_w + qb * 32 + l32;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const int d0 = kc * 16 + 8 * g;
+      u32x4_t w = {0u, 0u, 0u, 0u};
+      if (qi < L) {
+        w = *(const u32x4_t*)(qp + (int64_t)qi * a.q_l + d0);
+        if constexpr (ROT) {
+          const f32x4_t c = *(const f32x4_t*)(a.rc + (int64_t)qi * (D / 2) + d0 / 2);
+          const f32x4_t s = *(const f32x4_t*)(a.rs + (int64_t)qi * (D / 2) + d0 / 2);
+          w = rot4<DT>(w, c, s, a.q_scale);
+        } else {
+          w = scl4<DT>(w, a.q_scale);
+        }
+      }
+      qf[qb][kc] = w;
+    }
+  }
+  // fast-rho guard: the largest squared norm of the wave's queries (as the MFMA sees them; each
+  // lane holds half the features of query l32 of each block) against the key blocks it reads
+  bool fast = false;
+  if (!EXACT) {
+    float m = 0.0f;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float n2 = 0.0f;
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) n2 += chunk_norm2<DT>(qf[qb][kc]);
+      m = __builtin_fmaxf(m, n2 + __shfl_xor(n2, 32));
+    }
+    fast = fast_rho_safe(a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr, 0, (kend_w + 63) / 64,
+                         wave_max(m), a.nb_lim);
+  }
+  if (fast) d64_body<DT, true>(a, lds_k, lds_v, qf, bh, qblk);
+  else d64_body<DT, false>(a, lds_k, lds_v, qf, bh, qblk);
+}
+
+template <int DT, bool EXACT, bool ROT>
 static hipError_t launch_d64(const FwdArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((afa_fwd_d64_kernel<DT, EXACT, ROT>), dim3(a.B * a.H * a.nqb), dim3(256), 0, stream, a);
   return hipGetLastError();
@@ -379,22 +439,22 @@ static hipError_t launch_d64(const FwdArgs& a, hipStream_t stream) {
 size_t krot_bytes(const FwdArgs& a, int head_dim) { return (size_t)a.B * a.H * a.L * head_dim * 2; }
 
 template <int D>
-static void krot_launch_d(int dtype, const FwdArgs& a, void* krot, hipStream_t stream) {
+static void krot_launch_d(int dtype, const FwdArgs& a, void* krot, float* nb2, hipStream_t stream) {
   const dim3 grid((unsigned)((a.L + 63) / 64), (unsigned)(a.B * a.H));
   if (dtype == AFA_BF16)
-    hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2);
   else
-    hipLaunchKernelGGL((afa_krot_kernel<AFA_F16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot);
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_F16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2);
 }
 
-hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, hipStream_t stream) {
-  if (krot == nullptr) return hipErrorInvalidValue;
+hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, float* nb2, hipStream_t stream) {
+  if (krot == nullptr || nb2 == nullptr) return hipErrorInvalidValue;
   switch (head_dim) {
-    case 32: krot_launch_d<32>(dtype, a, krot, stream); break;
-    case 48: krot_launch_d<48>(dtype, a, krot, stream); break;
-    case 64: krot_launch_d<64>(dtype, a, krot, stream); break;
-    case 96: krot_launch_d<96>(dtype, a, krot, stream); break;
-    case 128: krot_launch_d<128>(dtype, a, krot, stream); break;
+    case 32: krot_launch_d<32>(dtype, a, krot, nb2, stream); break;
+    case 48: krot_launch_d<48>(dtype, a, krot, nb2, stream); break;
+    case 64: krot_launch_d<64>(dtype, a, krot, nb2, stream); break;
+    case 96: krot_launch_d<96>(dtype, a, krot, nb2, stream); break;
+    case 128: krot_launch_d<128>(dtype, a, krot, nb2, stream); break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
@@ -403,12 +463,15 @@ hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, hipStrea
   a.k_l = head_dim;
   a.k_h = (int64_t)a.L * head_dim;
   a.k_b = (int64_t)a.H * a.L * head_dim;
+  a.kbm = nb2;
+  a.nkb = (a.L + 63) / 64;
   return hipSuccess;
 }
 
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream) {
   a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
   a.w_unscale = 1.0f;
+  a.nb_lim = fast_rho_lim(1.0);  // s is the MFMA output itself
   const bool rot = a.rc != nullptr;
   if (dtype == AFA_BF16) {
     if (exact) return rot ? launch_d64<AFA_BF16, true, true>(a, stream) : launch_d64<AFA_BF16, true, false>(a, stream);

@@ -18,6 +18,8 @@
 //   * causal: each workgroup stops at its last query, each wave skips 32-key blocks past its
 //     own last query, and masks are evaluated only on blocks that cross the diagonal or
 //     valid_len.
+#include <cmath>
+
 #include "afa_common.h"
 #include "afa_launch.h"
 
@@ -127,6 +129,21 @@ void afa_fwd_mfma_kernel(const FwdArgs a) {
       qf[qb][kc] = w;
     }
   }
+  // fast-rho guard: the largest squared norm of the wave's queries as the MFMA sees them against
+  // the key blocks it reads
+  bool fast = false;
+  if (!EXACT) {
+    float m = 0.0f;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      float n2 = 0.0f;
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) n2 += chunk_norm2<DT>(qf[qb][kc]);
+      m = __builtin_fmaxf(m, n2 + __shfl_xor(n2, 32));
+    }
+    fast = fast_rho_safe(a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr, 0, (kend_w + 63) / 64,
+                         wave_max(m), a.nb_lim);
+  }
 
   // ---- tile loader (all 256 threads): chunk c = tid + 256 i -> key row c / C8, column c % C8
   u32x4_t kreg[NCH], vreg[NCH];
@@ -218,15 +235,17 @@ void afa_fwd_mfma_kernel(const FwdArgs a) {
           const int qlo = q0_w + qb * 32;
           const bool need_mask = (a.causal && key0 + 31 > qlo) || (key0 + 31 >= a.valid_len);
           float p[16];
+          if (fast) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float x = SM == 2 ? s[qb][r] * 1.41421356237309515f : s[qb][r];
-            if constexpr (EXACT) {
-              p[r] = rho8_exact(x);
-            } else if constexpr (SM == 1) {
-              p[r] = rho8_fast_half(x);
-            } else {
-              p[r] = rho8_fast(x);
+            for (int r = 0; r < 16; ++r) {
+              const float x = SM == 2 ? s[qb][r] * 1.41421356237309515f : s[qb][r];
+              p[r] = SM == 1 ? rho8_fast_half(x) : rho8_fast(x);
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float x = SM == 2 ? s[qb][r] * 1.41421356237309515f : s[qb][r];
+              p[r] = SM == 1 ? rho8_exact_half(x) : rho8_exact(x);
             }
           }
           if (need_mask) {
@@ -314,6 +333,9 @@ hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
   // either evaluate (rho/sqrt 2)^8 = rho^8/16 (bf16 fast path; weights and sink carry the
   // exact factor 1/16) or form s = sqrt(2) x per element.
   a.w_unscale = 1.0f;
+  // the key bounds come from the unrotated rows when the kernel rotates at tile load; the
+  // rounding of the rotated operands stays inside the bound's margin
+  a.nb_lim = fast_rho_lim(head_dim == 128 ? std::sqrt(2.0) : 1.0);
   if (head_dim == 64) {
     a.q_scale = 0.125f;
     if (dtype == AFA_BF16)

@@ -113,10 +113,18 @@ __device__ __attribute__((aligned(16))) unsigned int afa_pipe_zero_chunk[4];
 // SM: 0 = s as formed (q carries 1/sqrt(D) exactly, D = 64);
 //     1 = s = sqrt(2) x evaluated as (rho/sqrt 2)^8 = rho^8/16 (weights and sink carry 1/16);
 //     2 = s = a.s_mult x formed explicitly.
-template <int D, int DT, bool EXACT, int SM, bool ROT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PipeShape<padded_dim(D)>::WAVES_PER_EU,
-                                                                     PipeShape<padded_dim(D)>::WAVES_PER_EU)))
-void afa_fwd_pipe_kernel(const FwdArgs a) {
+// LDS tile of the pipelined kernels: 32 keys x the padded head dim.
+template <int DP>
+using PipeTile = unsigned short[32 * DP];
+
+// Tile loop and epilogue of afa_fwd_pipe_kernel for one form of rho^8: FAST, the branch-free
+// form (the wave's scores are all within the fast-rho bound), else the two-branch form.  The
+// kernel instantiates both and each wave runs one, so the two loops get their own register
+// allocation; the barriers count waves, not code locations.
+template <int D, int DT, bool FAST, int SM>
+__device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(D)>* lds_k,
+                                          PipeTile<padded_dim(D)>* lds_v, const u32x4_t (&qf)[padded_dim(D) / 16],
+                                          int bh, int qblk) {
   constexpr int DP = padded_dim(D);      // LDS row and MFMA width
   constexpr int KT = 32;                 // keys per tile = one unit
   constexpr int NB = PipeShape<DP>::NB;
@@ -126,19 +134,10 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
   constexpr int LOADS = 2 * LPT;
   constexpr int NK = DP / 16;            // 16-feature MFMA steps of S
   constexpr int NDB = DP / 32;           // 32-feature output blocks
-  static_assert(D % 16 == 0 && D <= DP, "head_dim");
-  static_assert(LPT >= 1 && KT * CH % 256 == 0, "tile loader shape");
-  static_assert(NB == 4, "the waits below assume at most one tile in flight beyond the next");
-  __shared__ __attribute__((aligned(16))) unsigned short lds_k[NB][KT * DP];
-  __shared__ __attribute__((aligned(16))) unsigned short lds_v[NB][KT * DP];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5, l16 = lane & 15, m16 = (lane >> 4) & 1;
-
-  int bh, qblk;
-  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
   const int b = bh / a.H, h = bh % a.H;
   const int L = a.L, vlen = a.valid_len;
   const int q0_wg = qblk * 128, q0_w = q0_wg + wave * 32;
@@ -146,24 +145,9 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
   const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
   const int ntiles = (kend_wg + KT - 1) / KT;
   const int U = q0_w < L ? (kend_w + KT - 1) / KT : 0;  // units of this wave
-  const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
+  const int qi = q0_w + l32;
   const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
-
-  // q fragments (B operand of S^T = K Q^T): query q0_w + l32, features kc*16 + 8g .. +7
-  const int qi = q0_w + l32;
-  u32x4_t qf[NK];
-#pragma unroll
-  for (int kc = 0; kc < NK; ++kc) {
-    u32x4_t w = {0u, 0u, 0u, 0u};
-    const int d0 = kc * 16 + 8 * g;
-    if (qi < L && d0 < D) {
-      const float* cc = ROT ? a.rc + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
-      const float* ss = ROT ? a.rs + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
-      w = q_chunk<DT, ROT>(*(const u32x4_t*)(qp + (int64_t)qi * a.q_l + d0), cc, ss, a.q_scale);
-    }
-    qf[kc] = w;
-  }
 
   // direct loads: slot s = tid + 256 i covers row s / CH, physical chunk s % CH
   auto issue_tile = [&](int t) {
@@ -248,12 +232,18 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
     float p[16];
+    if constexpr (FAST) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float x = SM == 2 ? scur[r] * a.s_mult : scur[r];
-      if constexpr (EXACT) p[r] = rho8_exact(x);
-      else if constexpr (SM == 1) p[r] = rho8_fast_half(x);
-      else p[r] = rho8_fast(x);
+      for (int r = 0; r < 16; ++r) {
+        const float x = SM == 2 ? scur[r] * a.s_mult : scur[r];
+        p[r] = SM == 1 ? rho8_fast_half(x) : rho8_fast(x);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = SM == 2 ? scur[r] * a.s_mult : scur[r];
+        p[r] = SM == 1 ? rho8_exact_half(x) : rho8_exact(x);
+      }
     }
     const int key0 = u * KT;
     if ((a.causal && key0 + 31 > q0_w) || key0 + 31 >= vlen) {
@@ -310,6 +300,67 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
   }
 }
 
+template <int D, int DT, bool EXACT, int SM, bool ROT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PipeShape<padded_dim(D)>::WAVES_PER_EU,
+                                                                     PipeShape<padded_dim(D)>::WAVES_PER_EU)))
+void afa_fwd_pipe_kernel(const FwdArgs a) {
+  constexpr int DP = padded_dim(D);      // LDS row and MFMA width
+  constexpr int KT = 32;                 // keys per tile = one unit
+  constexpr int NB = PipeShape<DP>::NB;
+  constexpr int CH = DP / 8;             // 16-byte chunks per LDS row
+  constexpr int CHD = D / 8;             // chunks that hold data
+  constexpr int LPT = KT * CH / 256;     // direct loads per thread per tile, each of K and V
+  constexpr int LOADS = 2 * LPT;
+  constexpr int NK = DP / 16;            // 16-feature MFMA steps of S
+  constexpr int NDB = DP / 32;           // 32-feature output blocks
+  static_assert(D % 16 == 0 && D <= DP, "head_dim");
+  static_assert(LPT >= 1 && KT * CH % 256 == 0, "tile loader shape");
+  static_assert(NB == 4, "the waits below assume at most one tile in flight beyond the next");
+  __shared__ __attribute__((aligned(16))) PipeTile<DP> lds_k[NB];
+  __shared__ __attribute__((aligned(16))) PipeTile<DP> lds_v[NB];
+
+  int bh, qblk;
+  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const int b = bh / a.H, h = bh % a.H;
+  const int L = a.L, vlen = a.valid_len;
+  const int q0_wg = qblk * 128, q0_w = q0_wg + wave * 32;
+  const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 128)) : vlen;
+  const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
+  const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
+
+  // q fragments (B operand of S^T = K Q^T): query q0_w + l32, features kc*16 + 8g .. +7
+  const int qi = q0_w + l32;
+  u32x4_t qf[NK];
+#pragma unroll
+  for (int kc = 0; kc < NK; ++kc) {
+    u32x4_t w = {0u, 0u, 0u, 0u};
+    const int d0 = kc * 16 + 8 * g;
+    if (qi < L && d0 < D) {
+      const float* cc = ROT ? a.rc + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
+      const float* ss = ROT ? a.rs + (int64_t)qi * (D / 2) + d0 / 2 : nullptr;
+      w = q_chunk<DT, ROT>(*(const u32x4_t*)(qp + (int64_t)qi * a.q_l + d0), cc, ss, a.q_scale);
+    }
+    qf[kc] = w;
+  }
+  // fast-rho guard: the largest squared norm of the wave's queries as the MFMA sees them (each
+  // lane holds half the features of query l32) against the key blocks it reads
+  bool fast = false;
+  if (!EXACT) {
+    float n2 = 0.0f;
+#pragma unroll
+    for (int kc = 0; kc < NK; ++kc) n2 += chunk_norm2<DT>(qf[kc]);
+    fast = fast_rho_safe(a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr, 0, (kend_w + 63) / 64,
+                         wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim);
+  }
+
+  if (fast) pipe_body<D, DT, true, SM>(a, lds_k, lds_v, qf, bh, qblk);
+  else pipe_body<D, DT, false, SM>(a, lds_k, lds_v, qf, bh, qblk);
+}
+
 namespace {
 
 template <int D, int DT, bool EXACT, int SM>
@@ -337,6 +388,7 @@ template <int D>
 hipError_t launch_scaled(int dtype, FwdArgs a, bool exact, int k, hipStream_t st) {
   a.q_scale = std::ldexp(1.0f, -k);
   a.s_mult = std::ldexp((float)(1.0 / std::sqrt((double)D)), k);
+  a.nb_lim = fast_rho_lim(a.s_mult);
   if (dtype == AFA_BF16) return exact ? launch_pipe<D, AFA_BF16, true, 2>(a, st) : launch_pipe<D, AFA_BF16, false, 2>(a, st);
   return exact ? launch_pipe<D, AFA_F16, true, 2>(a, st) : launch_pipe<D, AFA_F16, false, 2>(a, st);
 }
@@ -348,6 +400,7 @@ hipError_t launch_sqrt2(int dtype, FwdArgs a, bool exact, int k, hipStream_t st)
     a.q_scale = std::ldexp(1.0f, -k);
     a.omega *= 0.0625f;
     a.w_unscale = 16.0f;
+    a.nb_lim = fast_rho_lim(std::sqrt(2.0));  // s = sqrt(2) x
     return launch_pipe<D, AFA_BF16, false, 1>(a, st);
   }
   return launch_scaled<D>(dtype, a, exact, k, st);
@@ -364,6 +417,7 @@ hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
     case 48: return launch_scaled<48>(dtype, a, exact, 3, st);
     case 64:
       a.q_scale = 0.125f;  // 1/sqrt(64), exact in any binary format
+      a.nb_lim = fast_rho_lim(1.0);
       if (dtype == AFA_BF16) return exact ? launch_pipe<64, AFA_BF16, true, 0>(a, st) : launch_pipe<64, AFA_BF16, false, 0>(a, st);
       return exact ? launch_pipe<64, AFA_F16, true, 0>(a, st) : launch_pipe<64, AFA_F16, false, 0>(a, st);
     case 96: return launch_scaled<96>(dtype, a, exact, 4, st);

@@ -25,6 +25,13 @@ struct FwdArgs {
   float w_unscale;  // denominator output = w_unscale * (D' + omega)
   float s_mult;     // fp32 factor of the score after the q_scale fold (kernels that take one)
   float* part;      // split-K partials (afa_fwd_f32.hip): nsplit x B H L D numerators, then nsplit x B H L sums
+  // fast-rho guard (FastGuard in afa_common.h): the largest squared norm of the key rows of each
+  // 64-row block, nkb blocks per (b, h) (nullptr: every tile takes the two-branch rho), and the
+  // bound nb_lim on (squared query-fragment norm) x (key block bound) below which a tile's scores
+  // are all within |s| <= kFastRhoMaxScore (set by the launcher for its score scaling)
+  const float* kbm;
+  int nkb;
+  float nb_lim;
 };
 
 // Generic forward / backward (afa_generic.hip).
@@ -49,15 +56,29 @@ struct GenArgs {
   int exact_ref;
   double scale;
   double omega;
+  // fast-rho guard of the MFMA backward (as FwdArgs): per 64-row block bounds of q (for the dK/dV
+  // kernel, which owns keys) and of k (for the dQ kernel), nkb blocks per (b, h)
+  const float* qbm;
+  const float* kbm;
+  int nkb;
+  float nb_lim;
 };
 
 bool mfma_fwd_supported(int dtype, int head_dim);
 int mfma_fwd_queries_per_block(int head_dim);
 hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
 // K rotated once per call (afa_krot_kernel, head_dim 32, 48, 64, 96 or 128) into `krot`
-// (krot_bytes bytes, contiguous B, H, L, D); a's k then points at it.
+// (krot_bytes bytes, contiguous B, H, L, D); a's k then points at it, and a's key bounds at nb2
+// (B H ceil(L/64) floats), which the same launch fills from the rotated rows.
 size_t krot_bytes(const FwdArgs& a, int head_dim);
-hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, hipStream_t stream);
+hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, float* nb2, hipStream_t stream);
+// Bound of the fast-rho guard: kFastRhoMaxScore^2 / (score / MFMA-output)^2, less a 5% margin for
+// the rounding of the norms and of the rotated operands.
+float fast_rho_lim(double score_per_output);
+// Largest squared row norm of each 64-row block of x (bf16 / fp16; rows of head_dim elements,
+// 16-byte aligned, element strides per (b, h, l)) into nb2[bh * ceil(L/64) + block].
+hipError_t rownorm_launch(int dtype, const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                          int head_dim, float* nb2, hipStream_t stream);
 // Software-pipelined head_dim-64 kernel (afa_fwd_d64.hip); 256 queries per workgroup.  q is
 // rotated at load when a.rc is set; k must arrive rotated (krot_launch).
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);

@@ -341,10 +341,16 @@ def main():
     lib = _lib.lib()
     ptr = _lib.ptr
 
+    # the call's workspace (rotated k and the fast-rho key bounds), allocated once outside the
+    # timed region as a caller would
+    fws_bytes = lib.afa_fwd_workspace_size(code, B, H, L, D, int(rot is not None))
+    fws = torch.empty(max(fws_bytes, 1), dtype=torch.uint8, device=dev)
+
     def fwd():
         r = lib.afa_fwd(code, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), None,
                         out.data_ptr(), den.data_ptr() if backward else None, ptr(rc), ptr(rs),
-                        L if rot is not None else 0, 0.5, int(causal), 0, 0, stream.cuda_stream)
+                        L if rot is not None else 0, 0.5, int(causal), 0, 0, fws.data_ptr(), fws_bytes,
+                        stream.cuda_stream)
         if r != 0:
             _lib.check(r, "afa_fwd")
 
@@ -353,7 +359,7 @@ def main():
         fwd()
         gout = torch.randn((B, H, L, D), generator=g, device=dev, dtype=torch.float32).to(tdt)
         dq, dk, dv = (torch.empty_like(q) for _ in range(3))
-        ws_bytes = lib.afa_bwd_workspace_size(code, B, H, L, D)
+        ws_bytes = lib.afa_bwd_workspace_size(code, B, H, L, D, int(rot is not None))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
         def step():

@@ -2,7 +2,9 @@
  * afa.h — C ABI of the MI355X (gfx950) Algebraic FlashAttention library (libafa_hip.so).
  *
  * Every entry point takes plain device pointers, sizes and an optional hipStream_t
- * (passed as void*; NULL = the default stream).  The caller owns every buffer; calls are
+ * (passed as void*; NULL = the default stream).  The caller owns every buffer, including the
+ * workspaces of the entry points that take one (a NULL workspace makes the call allocate and
+ * free its own, stream-ordered, from a memory pool private to this library); calls are
  * stream-ordered, stateless and re-entrant.  They return 0 (AFA_OK) or an afa_status code;
  * afa_status_string() gives the message.
  *
@@ -44,7 +46,8 @@ enum afa_status {
 };
 
 /* Flags for afa_fwd / afa_bwd. */
-#define AFA_FLAG_EXACT_TAIL 0x1u   /* always use the cancellation-safe two-branch rho for s < 0 */
+#define AFA_FLAG_EXACT_TAIL 0x1u   /* always use the cancellation-safe two-branch rho for s < 0
+                                      (otherwise only where the fast-rho guard asks for it) */
 #define AFA_FLAG_GENERIC 0x2u      /* route to the generic (non-MFMA) kernel */
 #define AFA_FLAG_EXACT_REF 0x4u    /* exact_afa_reference contract: q*scale rounded to the input
                                       dtype before the dot, row sum of P cast to v.dtype, and
@@ -66,15 +69,25 @@ int afa_version(void);
  * fp32 (fp64 for AFA_F64); q and k rows at position i are rotated by row i (fusing
  * _rotate_tensor, src/attention.py:142-152, as called from src/model.py:262-264): q when the
  * kernel loads it, k at tile load, except on the pipelined bf16/fp16 paths (head_dim 32, 48,
- * 64, 96, 128), where k is rotated once per call into batch*heads*seq_len*head_dim elements of
- * stream-ordered scratch (hipMallocAsync, freed on `stream` before the call returns; if that
- * allocation fails the fully fused kernel runs instead at head_dim 64 and 128, the generic one
- * otherwise).  AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel (head_dim 64, 128).
+ * 64, 96, 128), where k is rotated once per call into the workspace.
+ * On bf16/fp16 inputs rho(s)^8 takes a branch-free form on key tiles where every score is
+ * provably within |s| <= 32 (Cauchy-Schwarz with per-block row norms that the call computes into
+ * the workspace), and the two-branch form of the reference elsewhere; AFA_FLAG_EXACT_TAIL forces
+ * the two-branch form everywhere.  AFA_FLAG_SIMPLE_SCHEDULE selects the fully fused kernel
+ * (head_dim 64, 128).
+ * workspace: at least afa_fwd_workspace_size() bytes of 16-byte aligned device memory for the
+ * same sizes and rotary choice (0 bytes on some paths), or NULL to let the call allocate it
+ * stream-ordered from a memory pool of this library and free it on `stream` before returning.
+ * The size is that of the call's largest path on the current device (the fp32 split-K partials
+ * depend on its compute-unit count).  Calls that share a workspace must be ordered on one stream.
  */
+size_t afa_fwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                              int64_t head_dim, int rotary);
 int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
             const void* q, const void* k, const void* v, const int64_t* strides, void* out,
             void* denom, const void* rot_cos, const void* rot_sin, int64_t rot_len,
-            double sink_omega, int causal, int64_t valid_len, unsigned flags, void* stream);
+            double sink_omega, int causal, int64_t valid_len, unsigned flags, void* workspace,
+            size_t workspace_bytes, void* stream);
 
 /*
  * Analytical AFA backward.  Replaces tiled_afa_backward (src/kernels/pallas_afa.py:409-522)
@@ -82,15 +95,13 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
  * denom (= d_total, fp32; fp64 for AFA_F64) and the output cotangent g (same layout as q).
  * Outputs dq, dk, dv (contiguous).  With rotary tables the forward rotated q and k, and the
  * returned dq, dk are with respect to the unrotated inputs (the fp32 matrix-core kernels rotate
- * them as tiles are staged); on the bf16/fp16 matrix-core path (head_dim 32, 48, 64, 96, 128,
- * 256) q and k are then rotated once into 2*batch*heads*seq_len*head_dim elements of
- * stream-ordered scratch (hipMallocAsync, freed on `stream` before the call returns; if that
- * allocation fails the generic kernel runs instead).  workspace: at least
- * afa_bwd_workspace_size() bytes of device memory, or NULL to let the call allocate and free
- * it on `stream`.
+ * them as tiles are staged; on the bf16/fp16 matrix-core path, head_dim 32, 48, 64, 96, 128 and
+ * 256, q and k are rotated once into the workspace).  rho(s)^8 follows the same fast-rho guard
+ * as afa_fwd.  workspace: at least afa_bwd_workspace_size() bytes (16-byte aligned) for the same
+ * sizes and rotary choice, or NULL to let the call allocate it as afa_fwd does.
  */
 size_t afa_bwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t seq_len,
-                              int64_t head_dim);
+                              int64_t head_dim, int rotary);
 int afa_bwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
             const void* q, const void* k, const void* v, const void* out, const void* denom,
             const void* g, void* dq, void* dk, void* dv, const void* rot_cos,

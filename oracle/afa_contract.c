@@ -335,17 +335,21 @@ int oracle_afa_bwd(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, const 
   if (valid_len <= 0 || valid_len > L) valid_len = L;
   const float scale = (float)(1.0 / sqrt((double)D));
   const float c8 = 8.0f * scale;
-#pragma omp parallel for schedule(dynamic, 1) num_threads(threads_for(nthreads))
+  const int threads = threads_for(nthreads);
+  float* Q = malloc(sizeof(float) * L * D);
+  float* K = malloc(sizeof(float) * L * D);
+  float* V = malloc(sizeof(float) * L * D);
+  float* G = malloc(sizeof(float) * L * D);
+  float* E = malloc(sizeof(float) * L);
+  float* aq = malloc(sizeof(float) * L * D);
+  float* ak = malloc(sizeof(float) * L * D);
+  float* av = malloc(sizeof(float) * L * D);
+  /* One head at a time; within a head the dq rows and the (dk, dv) rows are shared out over
+   * the threads, each pair (i, j) evaluated once per side.  Every output row accumulates its
+   * pairs in the same order as a single (i, j) sweep (dq_i over j, dk_j and dv_j over i), so
+   * the result does not depend on the thread count. */
   for (int64_t bh = 0; bh < B * H; ++bh) {
     const int64_t base = bh * L * D;
-    float* Q = malloc(sizeof(float) * L * D);
-    float* K = malloc(sizeof(float) * L * D);
-    float* V = malloc(sizeof(float) * L * D);
-    float* G = malloc(sizeof(float) * L * D);
-    float* E = malloc(sizeof(float) * L);
-    float* aq = calloc(L * D, sizeof(float));
-    float* ak = calloc(L * D, sizeof(float));
-    float* av = calloc(L * D, sizeof(float));
     load_rows(Q, q, dtype, base, 0, L, D, NULL, NULL);
     load_rows(K, k, dtype, base, 0, L, D, NULL, NULL);
     load_rows(V, v, dtype, base, 0, L, D, NULL, NULL);
@@ -355,32 +359,49 @@ int oracle_afa_bwd(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, const 
       for (int64_t d = 0; d < D; ++d) e += G[i * D + d] * load_in(out, base + i * D + d, dtype);
       E[i] = e;
     }
-    for (int64_t i = 0; i < L; ++i) {
-      const float di = d_total[bh * L + i];
-      for (int64_t j = 0; j < L; ++j) {
-        if (j >= valid_len || (causal && j > i)) continue;
-        float sdot = 0.0f, gw = 0.0f;
-        for (int64_t d = 0; d < D; ++d) sdot += Q[i * D + d] * K[j * D + d];
-        for (int64_t d = 0; d < D; ++d) gw += G[i * D + d] * V[j * D + d];
-        const float s = sdot * scale;
-        const float r = rsq1p_f32(s);
-        const float w = rho8_f32(s) / di;
-        const float ds = c8 * r * w * (gw - E[i]);
-        const float dsr = round_to(ds, dtype), wr = round_to(w, dtype);
-        for (int64_t d = 0; d < D; ++d) {
-          aq[i * D + d] += dsr * K[j * D + d];
-          ak[j * D + d] += dsr * Q[i * D + d];
-          av[j * D + d] += wr * G[i * D + d];
+#pragma omp parallel num_threads(threads)
+    {
+      /* ds and w of pair (i, j), rounded to the operand dtype */
+#define OAFA_PAIR(i, j, dsr, wr)                                                      \
+  float sdot = 0.0f, gw = 0.0f;                                                       \
+  for (int64_t d = 0; d < D; ++d) sdot += Q[(i) * D + d] * K[(j) * D + d];            \
+  for (int64_t d = 0; d < D; ++d) gw += G[(i) * D + d] * V[(j) * D + d];              \
+  const float s = sdot * scale;                                                       \
+  const float r = rsq1p_f32(s);                                                       \
+  const float w = rho8_f32(s) / d_total[bh * L + (i)];                                \
+  const float ds = c8 * r * w * (gw - E[(i)]);                                        \
+  const float dsr = round_to(ds, dtype), wr = round_to(w, dtype);
+#pragma omp for schedule(dynamic, 16)
+      for (int64_t i = 0; i < L; ++i) {
+        for (int64_t d = 0; d < D; ++d) aq[i * D + d] = 0.0f;
+        const int64_t jend = causal ? (i + 1 < valid_len ? i + 1 : valid_len) : valid_len;
+        for (int64_t j = 0; j < jend; ++j) {
+          OAFA_PAIR(i, j, dsr, wr)
+          (void)wr;
+          for (int64_t d = 0; d < D; ++d) aq[i * D + d] += dsr * K[j * D + d];
         }
       }
+#pragma omp for schedule(dynamic, 16)
+      for (int64_t j = 0; j < L; ++j) {
+        for (int64_t d = 0; d < D; ++d) ak[j * D + d] = av[j * D + d] = 0.0f;
+        if (j >= valid_len) continue;
+        for (int64_t i = causal ? j : 0; i < L; ++i) {
+          OAFA_PAIR(i, j, dsr, wr)
+          for (int64_t d = 0; d < D; ++d) {
+            ak[j * D + d] += dsr * Q[i * D + d];
+            av[j * D + d] += wr * G[i * D + d];
+          }
+        }
+      }
+#undef OAFA_PAIR
     }
     for (int64_t x = 0; x < L * D; ++x) {
       store_out(dq, base + x, aq[x], dtype);
       store_out(dk, base + x, ak[x], dtype);
       store_out(dv, base + x, av[x], dtype);
     }
-    free(Q); free(K); free(V); free(G); free(E); free(aq); free(ak); free(av);
   }
+  free(Q); free(K); free(V); free(G); free(E); free(aq); free(ak); free(av);
   return 0;
 }
 

@@ -32,7 +32,7 @@ def lib():
 
 def test_header_declares_the_boundary():
     names = _declared()
-    for n in ("afa_fwd", "afa_bwd", "afa_bwd_workspace_size", "asoftmax_fwd", "asoftmax_bwd",
+    for n in ("afa_fwd", "afa_fwd_workspace_size", "afa_bwd", "afa_bwd_workspace_size", "asoftmax_fwd", "asoftmax_bwd",
               "octic_fwd", "octic_bwd", "ago_build_tables", "ago_rotate", "afa_status_string",
               "afa_last_hip_error", "afa_version"):
         assert n in names
@@ -68,9 +68,9 @@ def test_status_strings(lib):
 
 
 def _fwd(lib, dtype=_lib.AFA_BF16, B=1, H=1, L=64, D=64, q=DUMMY, out=DUMMY, rc=None, rs=None,
-         rot_len=0, sink=0.5, valid=0):
+         rot_len=0, sink=0.5, valid=0, ws=None, ws_bytes=0):
     return lib.afa_fwd(dtype, B, H, L, D, q, DUMMY, DUMMY, None, out, None, rc, rs, rot_len, sink, 1,
-                       valid, 0, None)
+                       valid, 0, ws, ws_bytes, None)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -95,6 +95,38 @@ def test_afa_fwd_rejects_invalid_arguments(lib, kw, code):
     assert _fwd(lib, **kw) == code
 
 
+def test_afa_fwd_workspace_contract(lib):
+    """afa_fwd_workspace_size covers the call's largest path; a smaller caller workspace and a
+    misaligned one are refused before any device work."""
+    bf16 = lib.afa_fwd_workspace_size(_lib.AFA_BF16, 8, 12, 4096, 64, 0)
+    bf16_rot = lib.afa_fwd_workspace_size(_lib.AFA_BF16, 8, 12, 4096, 64, 1)
+    # key-norm bounds: B H ceil(L / 64) floats; the rotated k: B H L D bf16 elements more
+    assert bf16 >= 8 * 12 * 64 * 4
+    assert bf16_rot >= bf16 + 8 * 12 * 4096 * 64 * 2
+    assert lib.afa_fwd_workspace_size(_lib.AFA_F64, 8, 12, 4096, 64, 1) == 0
+    assert lib.afa_fwd_workspace_size(_lib.AFA_BF16, 0, 12, 4096, 64, 1) == 0
+    assert lib.afa_fwd_workspace_size(_lib.AFA_BF16, 1, 1, 64, 192, 0) == 0
+    need = lib.afa_fwd_workspace_size(_lib.AFA_BF16, 1, 1, 64, 64, 0)
+    assert need > 0
+    assert _fwd(lib, ws=DUMMY, ws_bytes=need - 1) == _lib.ERR_WORKSPACE
+    assert _fwd(lib, ws=DUMMY + 4, ws_bytes=need) == _lib.ERR_ALIGN
+    # the generic path (fp64) needs no workspace, so a zero-byte one passes validation; that call
+    # would launch, so only its size is checked here
+    assert lib.afa_fwd_workspace_size(_lib.AFA_F64, 1, 1, 64, 64, 0) == 0
+
+
+def test_afa_bwd_workspace_contract(lib):
+    plain = lib.afa_bwd_workspace_size(_lib.AFA_BF16, 2, 16, 8192, 128, 0)
+    rot = lib.afa_bwd_workspace_size(_lib.AFA_BF16, 2, 16, 8192, 128, 1)
+    # E and 1/d per row, the fast-rho bounds of q and k; with tables the rotated q and k
+    assert plain >= 2 * 16 * 8192 * 4 * 2 + 2 * 2 * 16 * 128 * 4
+    assert rot >= plain + 2 * 2 * 16 * 8192 * 128 * 2
+    f32 = lib.afa_bwd_workspace_size(_lib.AFA_F32, 2, 16, 8192, 128, 1)
+    assert f32 == lib.afa_bwd_workspace_size(_lib.AFA_F32, 2, 16, 8192, 128, 0) >= 2 * 16 * 8192 * 4 * 2
+    assert lib.afa_bwd(_lib.AFA_BF16, 1, 1, 64, 64, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY,
+                       None, None, 0, 0.5, 0, 0, 0, DUMMY, 16, None) == _lib.ERR_WORKSPACE
+
+
 def test_afa_bwd_rejects_invalid_arguments(lib):
     def bwd(dtype=_lib.AFA_BF16, D=64, g=DUMMY, sink=0.5, valid=0):
         return lib.afa_bwd(dtype, 1, 1, 64, D, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, g, DUMMY, DUMMY, DUMMY,
@@ -105,7 +137,7 @@ def test_afa_bwd_rejects_invalid_arguments(lib):
     assert bwd(D=200) == _lib.ERR_HEAD_DIM
     assert bwd(sink=-1.0) == _lib.ERR_SINK
     assert bwd(valid=99) == _lib.ERR_VALID_LEN
-    assert lib.afa_bwd_workspace_size(_lib.AFA_BF16, 2, 16, 8192, 128) > 0
+    assert lib.afa_bwd_workspace_size(_lib.AFA_BF16, 2, 16, 8192, 128, 0) > 0
 
 
 def test_asoftmax_octic_ago_reject_invalid_arguments(lib):

@@ -89,3 +89,26 @@ def test_flop_count_matches_definition():
     # 4 B H D N_pairs; non-causal is the reference's 4 b h l^2 d (scripts/run_phase6_tpu.py:236)
     assert A.afa_flops(8, 12, 4096, 64, True) == 4 * 8 * 12 * 64 * 4096 * 4097 // 2
     assert A.afa_flops(1, 4, 256, 64, False) == 4 * 4 * 256 * 256 * 64
+
+
+def test_rotary_tables_must_fit_the_head_dim():
+    """Cayley tables are (positions, head_dim / 2), up to broadcast axes of size 1; tables built for
+    another head dimension are refused instead of being reinterpreted as more rows (the reference's
+    alignment of the tables fails on the same mismatch, src/attention.py:110-139)."""
+    from algebraic_intelligence_amd._lib import table_2d
+    assert table_2d(torch.zeros(128, 32), 64).shape == (128, 32)
+    assert table_2d(torch.zeros(1, 1, 128, 32), 64).shape == (128, 32)
+    assert table_2d(torch.zeros(1, 128, 1, 32), 64).shape == (128, 32)
+    assert table_2d(torch.zeros(32), 64).shape == (1, 32)
+    for bad in (torch.zeros(128, 64), torch.zeros(128, 16), torch.zeros(2, 128, 32), torch.zeros(()),
+                torch.zeros(64 * 32)):
+        with pytest.raises(ValueError, match="head_dim/2"):
+            table_2d(bad, 64)
+    with pytest.raises(ValueError, match="even head dimension"):
+        table_2d(torch.zeros(8, 3), 7)
+    # both entry points check before any device work: a (L, 64) table with D = 64
+    q, k, v = _qkv((1, 1, 128, 64))
+    with pytest.raises(ValueError, match="head_dim/2"):
+        A.pallas_afa_forward(q, k, v, rotary_params=(torch.zeros(128, 64), torch.zeros(128, 64)))
+    with pytest.raises(ValueError, match="head_dim/2"):
+        A.apply_ago_rotations(q, k, (torch.zeros(128, 64), torch.zeros(128, 64)), seq_axis=2)

@@ -112,7 +112,7 @@ def _bwd_flags(q, k, v, out, den, g, causal, valid, flags, rot=None):
     B, H, L, D = q.shape
     dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
     code = _lib.dtype_code(q.dtype)
-    ws_bytes = _lib.lib().afa_bwd_workspace_size(code, B, H, L, D)
+    ws_bytes = _lib.lib().afa_bwd_workspace_size(code, B, H, L, D, int(rot is not None))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
     rc_p, rs_p, rlen = (None, None, 0) if rot is None else (rot[0].data_ptr(), rot[1].data_ptr(), rot[0].shape[0])
     rc = _lib.lib().afa_bwd(code, B, H, L, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
