@@ -99,6 +99,10 @@ int check_rotary(const void* rc, const void* rs, int64_t rot_len, int64_t L, int
 
 }  // namespace
 
+namespace afa {
+int hip_status_code(hipError_t e) { return hip_status(e); }
+}  // namespace afa
+
 extern "C" {
 
 const char* afa_status_string(int status) {
@@ -116,6 +120,7 @@ const char* afa_status_string(int status) {
     case AFA_ERR_WORKSPACE: return "workspace too small";
     case AFA_ERR_UNSUPPORTED: return "combination not supported by this build";
     case AFA_ERR_GAMMA: return "gamma must be finite and strictly positive";
+    case AFA_ERR_SCRATCH_LIMIT: return "the call needs more workspace than afa_fwd_noalloc's fixed scratch";
     case AFA_ERR_HIP: return "HIP runtime error";
     default: return "unknown status";
   }

@@ -64,6 +64,9 @@ struct GenArgs {
   float nb_lim;
 };
 
+// afa_status code of a HIP error (AFA_ERR_HIP, recording it for afa_last_hip_error).
+int hip_status_code(hipError_t e);
+
 bool mfma_fwd_supported(int dtype, int head_dim);
 int mfma_fwd_queries_per_block(int head_dim);
 hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);

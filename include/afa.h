@@ -42,6 +42,8 @@ enum afa_status {
   AFA_ERR_WORKSPACE = 10,    /* workspace too small */
   AFA_ERR_UNSUPPORTED = 11,  /* combination this build does not implement */
   AFA_ERR_GAMMA = 12,        /* OACE gamma not finite or not positive (src/loss.py:33-34) */
+  AFA_ERR_SCRATCH_LIMIT = 13, /* afa_fwd_noalloc: the call needs more workspace than the fixed
+                                 per-device scratch (AFA_NOALLOC_SCRATCH_BYTES) */
   AFA_ERR_HIP = 100          /* a HIP runtime call failed; afa_last_hip_error() has the code */
 };
 
@@ -88,6 +90,24 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
             void* denom, const void* rot_cos, const void* rot_sin, int64_t rot_len,
             double sink_omega, int causal, int64_t valid_len, unsigned flags, void* workspace,
             size_t workspace_bytes, void* stream);
+
+/*
+ * afa_fwd without allocation.  No counterpart in the reference: for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as afa_fwd; the workspace is a fixed array of
+ * AFA_NOALLOC_SCRATCH_BYTES that the library holds on every device it runs on until the process
+ * ends, and the call allocates nothing (no hipMalloc, hipFree or pool allocation).  Calls whose
+ * afa_fwd_workspace_size() exceeds the array return AFA_ERR_SCRATCH_LIMIT before any device work
+ * (64 MiB holds, e.g., B=8 H=12 L=4096 D=64 bf16 with rotary tables).  Every call on a device
+ * shares that device's array: calls that overlap on one device (different streams, or threads
+ * without ordering) race; calls ordered on one stream do not.  No part of the array needs to be
+ * cleared between calls.
+ */
+#define AFA_NOALLOC_SCRATCH_BYTES (64u << 20)
+int afa_fwd_noalloc(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                    const void* q, const void* k, const void* v, const int64_t* strides, void* out,
+                    void* denom, const void* rot_cos, const void* rot_sin, int64_t rot_len,
+                    double sink_omega, int causal, int64_t valid_len, unsigned flags, void* stream);
 
 /*
  * Analytical AFA backward.  Replaces tiled_afa_backward (src/kernels/pallas_afa.py:409-522)

@@ -61,7 +61,7 @@ def test_kernel_names_unique_across_sources(lib):
 def test_status_strings(lib):
     codes = [_lib.OK, _lib.ERR_NULL, _lib.ERR_DTYPE, _lib.ERR_SHAPE, _lib.ERR_HEAD_DIM, _lib.ERR_SINK,
              _lib.ERR_VALID_LEN, _lib.ERR_EPS, _lib.ERR_ROTARY, _lib.ERR_ALIGN, _lib.ERR_WORKSPACE,
-             _lib.ERR_UNSUPPORTED, _lib.ERR_GAMMA, _lib.ERR_HIP]
+             _lib.ERR_UNSUPPORTED, _lib.ERR_GAMMA, _lib.ERR_SCRATCH_LIMIT, _lib.ERR_HIP]
     texts = [lib.afa_status_string(c).decode() for c in codes]
     assert all(texts) and len(set(texts)) == len(texts)
     assert lib.afa_status_string(12345).decode()
