@@ -159,15 +159,38 @@ __device__ __forceinline__ float chunk_norm2(u32x4_t w) {
   float s = 0.0f;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
+    // the element goes through a scalar: this hipcc (clang 22, ROCm 7.2) compiles
+    // __builtin_bit_cast(T, w[p]) on a vector element as a cast of w[0] for every p
+    const unsigned u = w[p];
     if constexpr (DT == AFA_BF16) {
-      const bf16x2_t v = __builtin_bit_cast(bf16x2_t, w[p]);
+      const bf16x2_t v = __builtin_bit_cast(bf16x2_t, u);
       s = __builtin_amdgcn_fdot2_f32_bf16(v, v, s, false);
     } else {
-      const f16x2_t v = __builtin_bit_cast(f16x2_t, w[p]);
+      const f16x2_t v = __builtin_bit_cast(f16x2_t, u);
       s = __builtin_amdgcn_fdot2(v, v, s, false);
     }
   }
   return s;
+}
+
+// Lane layout of the row-norm producers (afa_rownorm_kernel, afa_krot_kernel): one wave covers
+// one block of 64 rows of D elements in CHP iterations; in each, CHP consecutive lanes hold the
+// 16-byte chunks of one row (chunks c >= D/8 idle when D/8 is not a power of two), so 64 / CHP
+// rows are read as one contiguous span and a row's sum needs log2(CHP) shuffles.
+template <int D>
+struct RowBlockLayout {
+  static constexpr int CH = D / 8;
+  static constexpr int CHP = CH <= 4 ? 4 : CH <= 8 ? 8 : CH <= 16 ? 16 : 32;
+  static constexpr int RPI = 64 / CHP;  // rows per iteration
+  static_assert(D % 8 == 0 && CH <= 32, "row layout");
+};
+
+// Sum of v over the n consecutive lanes (n a power of two, aligned) that share it.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < N; o <<= 1) v += __shfl_xor(v, o);
+  return v;
 }
 
 // Maximum of a per-lane value over the wave, returned wave-uniform.

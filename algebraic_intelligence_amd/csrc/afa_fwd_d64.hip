@@ -93,38 +93,54 @@ __host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 
 
 // Cayley rotation of K, once per call: y (contiguous B, H, L, D) = rotate(x) in fp32 with the
 // (L, D/2) fp32 tables, rounded once to the element type -- the values the fused loaders would
-// produce (rot4 with scale 1).  Grid (ceil(L / 64), B * H); a block rotates 64 key rows, thread
-// slot e = tid + 256 i covering row e / (D/8), 16-byte chunk e % (D/8).  It also writes the
-// largest squared norm of the block's rotated rows (as rounded) to nb2[bh * gridDim.x + block],
-// the key bound of the fast-rho guard.
+// produce (rot4 with scale 1).  Each wave handles one (b, h, 64-row block) work item with the
+// lane layout of RowBlockLayout (contiguous 16-byte chunks), and also writes the largest squared
+// norm of the block's rotated rows (as rounded) to nb2[bh * nblk + block], the key bound of the
+// fast-rho guard (fast_rho_safe).
 template <int DT, int D>
-__global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y, float* nb2) {
-  constexpr int CH = D / 8;
-  __shared__ float rn[64];
-  const int bh = blockIdx.y;
-  const int b = bh / a.H, h = bh % a.H;
+__global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y, float* nb2, int nblk,
+                                                      int nwork) {
+  using RL = RowBlockLayout<D>;
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * 4 + (int)(threadIdx.x >> 6);  // wave-uniform work item
+  if (w >= nwork) return;
+  const int bh = w / nblk, blk = w - bh * nblk;
+  const int b = bh / a.H, h = bh - b * a.H;
   const unsigned short* xb = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   unsigned short* yb = y + (int64_t)bh * a.L * D;
-  if (threadIdx.x < 64) rn[threadIdx.x] = 0.0f;
-  __syncthreads();
+  const int c = lane % RL::CHP, rsub = lane / RL::CHP;
+  // the loads of G row iterations are issued before their first store: the stores to y could
+  // alias the inputs as far as the compiler knows, so a load-rotate-store loop would wait on HBM
+  // per row; G = 4 keeps 12 loads per lane in flight at 48 VGPRs of staging
+  constexpr int G = RL::CHP < 4 ? RL::CHP : 4;
+  float m = 0.0f;
 #pragma unroll
-  for (int i = 0; i < (64 * CH + 255) / 256; ++i) {
-    const int e = threadIdx.x + 256 * i;
-    const int l = blockIdx.x * 64 + e / CH, ch = e % CH;
-    if (e < 64 * CH && l < a.L) {
-      const u32x4_t w = *(const u32x4_t*)(xb + (int64_t)l * a.k_l + ch * 8);
-      const f32x4_t cc = *(const f32x4_t*)(a.rc + (int64_t)l * (D / 2) + ch * 4);
-      const f32x4_t ss = *(const f32x4_t*)(a.rs + (int64_t)l * (D / 2) + ch * 4);
-      const u32x4_t r = rot4<DT>(w, cc, ss, 1.0f);
-      *(u32x4_t*)(yb + (int64_t)l * D + ch * 8) = r;
-      atomicAdd(&rn[e / CH], chunk_norm2<DT>(r));
+  for (int g = 0; g < RL::CHP; g += G) {
+    u32x4_t wv[G];
+    f32x4_t cc[G], ss[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int l = blk * 64 + (g + i) * RL::RPI + rsub;
+      if (c < RL::CH && l < a.L) {
+        wv[i] = *(const u32x4_t*)(xb + (int64_t)l * a.k_l + c * 8);
+        cc[i] = *(const f32x4_t*)(a.rc + (int64_t)l * (D / 2) + c * 4);
+        ss[i] = *(const f32x4_t*)(a.rs + (int64_t)l * (D / 2) + c * 4);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int l = blk * 64 + (g + i) * RL::RPI + rsub;
+      float n2 = 0.0f;
+      if (c < RL::CH && l < a.L) {
+        const u32x4_t r = rot4<DT>(wv[i], cc[i], ss[i], 1.0f);
+        *(u32x4_t*)(yb + (int64_t)l * D + c * 8) = r;
+        n2 = chunk_norm2<DT>(r);
+      }
+      m = __builtin_fmaxf(m, group_sum<RL::CHP>(n2));
     }
   }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const float m = wave_max(rn[threadIdx.x]);
-    if (threadIdx.x == 0) nb2[(int64_t)bh * gridDim.x + blockIdx.x] = m;
-  }
+  m = wave_max(m);
+  if (lane == 0) nb2[(int64_t)bh * nblk + blk] = m;
 }
 
 // Tile loop and epilogue of afa_fwd_d64_kernel for one form of rho^8: FAST, the branch-free
@@ -440,11 +456,15 @@ size_t krot_bytes(const FwdArgs& a, int head_dim) { return (size_t)a.B * a.H * a
 
 template <int D>
 static void krot_launch_d(int dtype, const FwdArgs& a, void* krot, float* nb2, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.L + 63) / 64), (unsigned)(a.B * a.H));
+  const int nblk = (a.L + 63) / 64;
+  const int nwork = a.B * a.H * nblk;
+  const dim3 grid((unsigned)((nwork + 3) / 4));
   if (dtype == AFA_BF16)
-    hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2);
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2,
+                       nblk, nwork);
   else
-    hipLaunchKernelGGL((afa_krot_kernel<AFA_F16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2);
+    hipLaunchKernelGGL((afa_krot_kernel<AFA_F16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2,
+                       nblk, nwork);
 }
 
 hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, float* nb2, hipStream_t stream) {

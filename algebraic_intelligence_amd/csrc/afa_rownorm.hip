@@ -1,4 +1,4 @@
-// Row-norm pre-pass of the fast-rho guard (FastGuard in afa_common.h).
+// Row-norm pre-pass of the fast-rho guard (fast_rho_safe in afa_common.h).
 //
 // For every (b, h) and every block of 64 rows, the largest squared norm of the block's rows,
 // sum_d x_ld^2 in fp32 from the bf16 / fp16 elements as stored.  The MFMA kernels bound every
@@ -13,29 +13,56 @@
 
 namespace afa {
 
-// Grid (ceil(L / 64), B * H), 256 threads; thread slot e = tid + 256 i covers row e / (D/8) of the
-// block and its 16-byte chunk e % (D/8).  Partial sums meet in LDS (the order of the fp32 adds
-// does not matter to a bound that carries a margin).
-template <int DT>
+// Each wave handles one (b, h, 64-row block) work item (RowBlockLayout): CHP loads per lane
+// issued back to back, then the row sums by shuffles and the wave maximum.  No LDS, no barrier.
+template <int DT, int D>
 __global__ __launch_bounds__(256) void afa_rownorm_kernel(const unsigned short* x, int64_t sb, int64_t sh,
-                                                         int64_t sl, int H, int L, int D, float* nb2) {
-  __shared__ float rn[64];
-  const int bh = blockIdx.y;
-  const int b = bh / H, h = bh % H;
-  const int ch = D / 8;
+                                                         int64_t sl, int H, int L, int nblk, int nwork,
+                                                         float* nb2) {
+  using RL = RowBlockLayout<D>;
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * 4 + (int)(threadIdx.x >> 6);  // wave-uniform work item
+  if (w >= nwork) return;
+  const int bh = w / nblk, blk = w - bh * nblk;
+  const int b = bh / H, h = bh - b * H;
   const unsigned short* xb = x + b * sb + h * sh;
-  if (threadIdx.x < 64) rn[threadIdx.x] = 0.0f;
-  __syncthreads();
-  for (int e = threadIdx.x; e < 64 * ch; e += 256) {
-    const int r = e / ch, c = e - r * ch;
-    const int l = blockIdx.x * 64 + r;
-    if (l < L) atomicAdd(&rn[r], chunk_norm2<DT>(*(const u32x4_t*)(xb + (int64_t)l * sl + c * 8)));
+  const int c = lane % RL::CHP, rsub = lane / RL::CHP;
+  u32x4_t v[RL::CHP];
+#pragma unroll
+  for (int it = 0; it < RL::CHP; ++it) {
+    const int row = blk * 64 + it * RL::RPI + rsub;
+    v[it] = u32x4_t{0u, 0u, 0u, 0u};
+    if (c < RL::CH && row < L) v[it] = *(const u32x4_t*)(xb + (int64_t)row * sl + c * 8);
   }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const float m = wave_max(rn[threadIdx.x]);
-    if (threadIdx.x == 0) nb2[(int64_t)bh * gridDim.x + blockIdx.x] = m;
+  float m = 0.0f;
+#pragma unroll
+  for (int it = 0; it < RL::CHP; ++it) m = __builtin_fmaxf(m, group_sum<RL::CHP>(chunk_norm2<DT>(v[it])));
+  m = wave_max(m);
+  if (lane == 0) nb2[(int64_t)bh * nblk + blk] = m;
+}
+
+template <int DT, int D>
+static void rownorm_launch_d(const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, float* nb2,
+                             hipStream_t stream) {
+  const int nblk = (L + 63) / 64;
+  const int nwork = B * H * nblk;
+  hipLaunchKernelGGL((afa_rownorm_kernel<DT, D>), dim3((unsigned)((nwork + 3) / 4)), dim3(256), 0, stream,
+                     (const unsigned short*)x, sb, sh, sl, H, L, nblk, nwork, nb2);
+}
+
+template <int DT>
+static hipError_t rownorm_launch_dt(const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
+                                    int head_dim, float* nb2, hipStream_t stream) {
+  switch (head_dim) {
+    case 32: rownorm_launch_d<DT, 32>(x, sb, sh, sl, B, H, L, nb2, stream); break;
+    case 48: rownorm_launch_d<DT, 48>(x, sb, sh, sl, B, H, L, nb2, stream); break;
+    case 64: rownorm_launch_d<DT, 64>(x, sb, sh, sl, B, H, L, nb2, stream); break;
+    case 96: rownorm_launch_d<DT, 96>(x, sb, sh, sl, B, H, L, nb2, stream); break;
+    case 128: rownorm_launch_d<DT, 128>(x, sb, sh, sl, B, H, L, nb2, stream); break;
+    case 256: rownorm_launch_d<DT, 256>(x, sb, sh, sl, B, H, L, nb2, stream); break;
+    default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
 }
 
 float fast_rho_lim(double score_per_output) {
@@ -45,17 +72,10 @@ float fast_rho_lim(double score_per_output) {
 
 hipError_t rownorm_launch(int dtype, const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
                           int head_dim, float* nb2, hipStream_t stream) {
-  if (x == nullptr || nb2 == nullptr || head_dim % 8 != 0 || head_dim > 256) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((L + 63) / 64), (unsigned)(B * H));
-  if (dtype == AFA_BF16)
-    hipLaunchKernelGGL((afa_rownorm_kernel<AFA_BF16>), grid, dim3(256), 0, stream, (const unsigned short*)x, sb, sh,
-                       sl, H, L, head_dim, nb2);
-  else if (dtype == AFA_F16)
-    hipLaunchKernelGGL((afa_rownorm_kernel<AFA_F16>), grid, dim3(256), 0, stream, (const unsigned short*)x, sb, sh,
-                       sl, H, L, head_dim, nb2);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (x == nullptr || nb2 == nullptr) return hipErrorInvalidValue;
+  if (dtype == AFA_BF16) return rownorm_launch_dt<AFA_BF16>(x, sb, sh, sl, B, H, L, head_dim, nb2, stream);
+  if (dtype == AFA_F16) return rownorm_launch_dt<AFA_F16>(x, sb, sh, sl, B, H, L, head_dim, nb2, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace afa

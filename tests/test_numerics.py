@@ -59,3 +59,15 @@ def test_fast_rho8_fails_far_outside_the_guard():
     fast = _fast_rho8_f32(s, 1)
     assert np.all(exact < 1e-50)
     assert fast[0] > 1e-9 and fast[1] > 1e-2
+
+
+def test_fast_rho8_is_off_by_factors_near_minus_1500():
+    """The premise of the GPU tests whose rows score near -1500: there |s| eta ~ rho(s), so most
+    branch-free weights are off by more than 50% (for every rsqrt rounding), some by factors of
+    100 or more, and a per-row check at 1e-2 or 3e-2 fails if the guard let that form run."""
+    s = -np.linspace(1000.0, 2000.0, 20001).astype(np.float32)
+    exact = O.rho8(s.astype(np.float64))
+    for ulps in (-1, 0, 1):
+        ratio = _fast_rho8_f32(s, ulps) / exact
+        assert np.mean(np.abs(ratio - 1.0) > 0.5) > 0.5
+    assert (_fast_rho8_f32(s, 1) / exact).max() > 100.0

@@ -168,12 +168,15 @@ def test_bf16_denominator_is_fp32_sum_of_unrounded_weights(shape):
 
 
 # ----------------------------------------------------------------------------------- negative rows
-def _negative_rows(B, H, L, D, dt, c, seed, n_neg):
+def _negative_rows(B, H, L, D, dt, c, seed, n_neg, hollow=False):
     """q, k, v where the first n_neg queries of every head score about -c sqrt(D) against every
     key: k_j = u + 0.02 n_j and q_i = -c u (1 + 0.002 m_i) with |u|^2 = D, so
-    s_ij = q_i . k_j / sqrt(D) ~ -c |u|^2 / sqrt(D).  The other queries are N(0, 1)."""
+    s_ij = q_i . k_j / sqrt(D) ~ -c |u|^2 / sqrt(D).  The other queries are N(0, 1).  hollow:
+    u is zero on the first two elements of every 8 (the first 4 bytes of every 16-byte chunk)."""
     rng = np.random.default_rng(seed)
     u = rng.standard_normal(D)
+    if hollow:
+        u[np.arange(D) % 8 < 2] = 0.0
     u *= np.sqrt(D) / np.linalg.norm(u)
     k = u + 0.02 * rng.standard_normal((B, H, L, D))
     q = rng.standard_normal((B, H, L, D))
@@ -221,6 +224,71 @@ def test_all_negative_rows_per_row(c, label, shape, flags):
         assert err.max() <= 1e-2
         # the other rows as usual
         assert normwise(to_f64(out[b, h, n_neg:]), ref[n_neg:]) <= 2e-2
+
+
+def _identity_tables(L, D):
+    """Rotary tables of the identity rotation (c = 1, s = 0): the rotary code paths (k rotated
+    once per call, q at load, the backward's rotation pre-pass) run and the scores stay those of
+    the unrotated rows."""
+    return torch.ones(L, D // 2, device=DEV), torch.zeros(L, D // 2, device=DEV)
+
+
+@pytest.mark.parametrize("rotary", [False, True], ids=["plain", "rotary"])
+@pytest.mark.parametrize("shape,flags", [((1, 2, 256, 64), 0), ((2, 384, 256, 64), 0), ((1, 2, 256, 128), 0),
+                                         ((1, 2, 256, 96), 0), ((1, 2, 256, 64), _lib.FLAG_SIMPLE_SCHEDULE)])
+def test_guard_sees_every_feature(shape, flags, rotary):
+    """Rows near s = -1500 whose q and k are zero on the first 4 bytes of every 16-byte chunk.
+    The guard's row norms must cover every element: a norm that read one 4-byte word per chunk
+    would be 0 here (a miscompile of __builtin_bit_cast on a vector element did exactly that),
+    the guard would pass the branch-free rho^8, and its weights would be off by factors
+    (|s| eta ~ rho(s) at |s| ~ 1500).  Per row against float64 to 1e-2, as above."""
+    B, H, L, D = shape
+    n_neg = 40
+    q, k, v = _negative_rows(B, H, L, D, torch.bfloat16, 190.0 * 8.0 / np.sqrt(D), seed=41 + D, n_neg=n_neg,
+                             hollow=True)
+    out, den = _fwd(q, k, v, causal=True, rotary=_identity_tables(L, D) if rotary else None, flags=flags)
+    for b, h in [(0, 0), (B - 1, H - 1)]:
+        qh, kh, vh = to_f64(q[b, h]), to_f64(k[b, h]), to_f64(v[b, h])
+        assert np.all(qh[:n_neg, np.arange(D) % 8 < 2] == 0.0)
+        s = qh[:n_neg] @ kh.T / np.sqrt(D)
+        ref = O.afa_forward(qh, kh, vh, 0.5, True)
+        err = _row_errors(out[b, h, :n_neg], ref[:n_neg])
+        print(f"{shape} flags={flags} rotary={rotary}: hollow rows, scores up to {s.max():.1f}, "
+              f"worst per-row error {err.max():.2e}")
+        assert s.max() < -1000.0
+        assert err.max() <= 1e-2
+        assert normwise(to_f64(out[b, h, n_neg:]), ref[n_neg:]) <= 2e-2
+
+
+@pytest.mark.parametrize("rotary", [False, True], ids=["plain", "rotary"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_guard_sees_every_feature_backward(D, rotary):
+    """The backward's guards (dq: the wave's q rows against the key-block norms; dk/dv: the
+    wave's k rows against the query-block norms) on hollow rows where every score is near -1500,
+    so that dq, dk and dv all come from weights the branch-free form would get wrong: every row
+    of each against the C restatement of the contract, relative to the row.  dv_j sums
+    w_ij g_i / d_i and is well conditioned: 1e-2.  dq_i and dk_j sum ds_ij k_j and ds_ij q_i of
+    both signs over near-parallel rows after ds is rounded to bf16, so single rounding flips of
+    ds show: the contract itself is up to 0.1 (dq) and 0.2 (dk) off float64 per row on these
+    inputs, and the bound against it is 3e-2.  Weights of the branch-free form would be off by
+    factors."""
+    B, H, L = 1, 2, 256
+    q, k, v = _negative_rows(B, H, L, D, torch.bfloat16, 190.0 * 8.0 / np.sqrt(D), seed=43 + D, n_neg=L,
+                             hollow=True)
+    rot = _identity_tables(L, D) if rotary else None
+    out, den = _fwd(q, k, v, causal=True, rotary=rot)
+    g = make_qkv((B, H, L, D), torch.bfloat16, seed=44)[0]
+    dq, dk, dv = A.tiled_afa_backward(q, k, v, out, den, g, 0.5, True, rotary_params=rot)
+    cq, ck, cv = C.afa_bwd(to_bits(q), to_bits(k), to_bits(v), to_bits(out),
+                           den.detach().cpu().numpy().astype(np.float32).reshape(B, H, L), to_bits(g), C.DT_BF16, True)
+    s = to_f64(q[0, 0]) @ to_f64(k[0, 0]).T / np.sqrt(D)
+    assert s[np.tril(np.ones((L, L), bool))].max() < -1000.0
+    for name, got, ref in (("dq", dq, cq), ("dk", dk, ck), ("dv", dv, cv)):
+        ref = C.to_f32(ref, C.DT_BF16).astype(np.float64)
+        err = _row_errors(got.reshape(-1, D), ref.reshape(-1, D))
+        print(f"backward D={D} rotary={rotary}, hollow rows near s = -1500: worst per-row {name} error {err.max():.2e}")
+        assert np.isfinite(to_f64(got)).all()
+        assert err.max() <= (1e-2 if name == "dv" else 3e-2), name
 
 
 @pytest.mark.parametrize("shape", [(1, 2, 256, 64), (2, 384, 256, 64), (1, 2, 256, 128)])
