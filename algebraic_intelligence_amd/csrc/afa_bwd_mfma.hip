@@ -120,8 +120,6 @@ __device__ __forceinline__ void unrotate4(f32x16_t& acc, int e0, const float* rc
   }
 }
 
-__host__ __device__ constexpr int vm_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-
 // rho(s)^8 and r = rsqrt(1 + s^2).  EXACT: two-branch (rho(|s|)^8, reciprocal for s < 0);
 // otherwise the branch-free form, used on tiles the fast-rho guard clears (FastGuard).
 template <bool EXACT>
@@ -295,13 +293,13 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       if constexpr (D < DP) {
         if (lc >= D / 8) ks = vs = (const void*)afa_bwd_zero_chunk;
       }
-      __builtin_amdgcn_global_load_lds(ks, (void*)kd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vs, (void*)vd, 16, 0, 0);
+      lds_dma16(ks, kd);
+      lds_dma16(vs, vd);
     }
   };
 
   if (ntiles > 0) issue(0);
-  __builtin_amdgcn_s_waitcnt(vm_only(0));
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
@@ -357,7 +355,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
             dq[fb] = bmma<DT>(frag_tr<DP>(tk, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dq[fb]);
       }
     }
-    __builtin_amdgcn_s_waitcnt(vm_only(0));
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
   }
 
@@ -465,8 +463,8 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       if constexpr (D < DP) {
         if (lc >= D / 8) qs = gs = (const void*)afa_bwd_zero_chunk;
       }
-      __builtin_amdgcn_global_load_lds(qs, (void*)qd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(gs, (void*)gd, 16, 0, 0);
+      lds_dma16(qs, qd);
+      lds_dma16(gs, gd);
     }
     if (wave == 0 && lane < 2 * LPE) {
       // LPE lanes of E, LPE of 1/d: 4 rows per lane (the head's LP rows are a whole number of
@@ -474,12 +472,12 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       const int rr = t * QT + (lane % LPE) * 4;
       const int r0 = rr < LP ? rr : LP - 4;
       const float* src = (lane < LPE ? ep : ip) + r0;
-      __builtin_amdgcn_global_load_lds((const void*)src, (void*)&lds_ei[t & 1][0], 16, 0, 0);
+      lds_dma16(src, &lds_ei[t & 1][0]);
     }
   };
 
   if (t0 < ntiles) issue(t0);
-  __builtin_amdgcn_s_waitcnt(vm_only(0));
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
 
   for (int t = t0; t < ntiles; ++t) {
@@ -552,7 +550,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           }
       }
     }
-    __builtin_amdgcn_s_waitcnt(vm_only(0));
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
   }
 
@@ -648,7 +646,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       if constexpr (D < DP) {
         if (lc >= D / 8) vs = (const void*)afa_bwd_zero_chunk;
       }
-      __builtin_amdgcn_global_load_lds(vs, (void*)&lds_vk[(256 * i + wave * 64) * 8], 16, 0, 0);
+      lds_dma16(vs, &lds_vk[(256 * i + wave * 64) * 8]);
     }
   }
   // fast-rho guard: the largest squared norm of the wave's k / 8 rows against the query blocks

@@ -193,6 +193,31 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane i of the wave
+// reads sbase + voff (voff per lane, sbase wave-uniform) and writes LDS bytes lds + 16 i
+// (lds wave-uniform, M0).  Issued as inline assembly so that the compiler does not track it:
+// this hipcc waits for every LDS-DMA load in flight before each ds_read_b64_tr_b16, whatever
+// LDS it reads, which stalls a wave on the tile it has just started loading.  A kernel using
+// this orders the loads against its LDS reads itself (s_waitcnt vmcnt, then a barrier, before
+// a buffer is read) and waits for them before it ends.
+__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, const void* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(m0)
+               : "memory", "m0");
+}
+
+// The same with a full 64-bit address per lane.
+__device__ __forceinline__ void lds_dma16(const void* src, const void* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9: vmcnt [3:0] and [15:14]; expcnt and
+// lgkmcnt at their no-wait maxima).
+__host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
 // Maximum of a per-lane value over the wave, returned wave-uniform.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -87,10 +87,6 @@ constexpr int D64_KT = 64;
 constexpr int D64_NB = 4;
 typedef unsigned short D64Tile[D64_KT * 64];
 
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9: vmcnt [3:0] and [15:14]; expcnt and
-// lgkmcnt at their no-wait maxima).
-__host__ __device__ constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-
 // Cayley rotation of K, once per call: y (contiguous B, H, L, D) = rotate(x) in fp32 with the
 // (L, D/2) fp32 tables, rounded once to the element type -- the values the fused loaders would
 // produce (rot4 with scale 1).  Each wave handles one (b, h, 64-row block) work item with the
@@ -199,10 +195,10 @@ __device__ __forceinline__ void d64_body(const FwdArgs& a, D64Tile* lds_k, D64Ti
     if (t * KT + KT <= L) {
       const char* vb = (const char*)vp + (int64_t)t * KT * a.v_l * 2;
       const char* kb = (const char*)kp + (int64_t)t * KT * a.k_l * 2;
-      __builtin_amdgcn_global_load_lds((const void*)(vb + voff), (void*)vdst, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vb + v32 + voff), (void*)(vdst + 2048), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(kb + koff), (void*)kdst, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(kb + k32 + koff), (void*)(kdst + 2048), 16, 0, 0);
+      lds_dma16(vb, voff, vdst);
+      lds_dma16(vb + v32, voff, vdst + 2048);
+      lds_dma16(kb, koff, kdst);
+      lds_dma16(kb + k32, koff, kdst + 2048);
     } else {
       // last, partial tile: rows past L read row L-1 (masked keys; the data only has to be finite)
 #pragma unroll
@@ -210,10 +206,8 @@ __device__ __forceinline__ void d64_body(const FwdArgs& a, D64Tile* lds_k, D64Ti
         const int key = min(t * KT + row0 + 32 * i, L - 1);
         const uint32_t vo = (uint32_t)(key * (int)a.v_l + lcv * 8) * 2u;
         const uint32_t ko = (uint32_t)(key * (int)a.k_l + lck * 8) * 2u;
-        __builtin_amdgcn_global_load_lds((const void*)((const char*)vp + vo), (void*)(vdst + 2048 * i),
-                                         16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)((const char*)kp + ko), (void*)(kdst + 2048 * i),
-                                         16, 0, 0);
+        lds_dma16(vp, vo, vdst + 2048 * i);
+        lds_dma16(kp, ko, kdst + 2048 * i);
       }
     }
   };
@@ -338,19 +332,67 @@ __device__ __forceinline__ void d64_body(const FwdArgs& a, D64Tile* lds_k, D64Ti
       }
     }
   };
+  // The same unit where it is known to be one of the wave's units, to need no mask and (even
+  // units) to have a next sub-tile.  With no branch, the 8 MFMAs, the rho^8 VALU, the row sum,
+  // the P packing and the fragment reads form one basic block, and the scheduler spreads the
+  // MFMAs through the VALU stream: the wave keeps issuing VALU while its MFMAs run, instead of
+  // waiting on the MFMA pipe before a branch.
+  auto clean_unit = [&](int u, f32x16_t& scur, f32x16_t& snxt, auto qb_tag) {
+    constexpr int QB = decltype(qb_tag)::value;
+    constexpr int NQ = QB ^ 1;
+    constexpr int PQ = QB ^ 1;
+    const int n = u >> 1;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) snxt[e] = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) snxt = mma<DT>(kf[kc], qf[NQ][kc], snxt);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) o[db][PQ] = mma<DT>(vf[db][kk], p_prev[kk], o[db][PQ]);
+    float p[16];
+    rho8_unit(p, scur);
+    finish_p(p, QB);
+    if constexpr (QB == 0) {
+      read_kf(n + 1, kf);
+      read_vf(n, vf);
+    }
+  };
+  // Units 4t+1 .. 4t+4 of tile iteration t are clean when the last two (the largest key
+  // sub-tile 2t+2 against either query half) need no mask and unit 4t+5 is still one of the
+  // wave's.  Each condition can only turn false as t grows, so the clean iterations are a prefix
+  // [0, tc): they run in a loop of their own (one loop holding both unit forms would not fit
+  // the register budget).  Every wave passes ntiles barriers.
+  auto tile_clean = [&](int t) {
+    const int key_hi = 64 * t + 95;  // last key of sub-tile 2t+2
+    return (!a.causal || key_hi <= q0_w) && key_hi < vlen && 4 * t + 5 < U;
+  };
+  int tc = 0;
+  while (tc < ntiles && tile_clean(tc)) ++tc;
 
   // Iteration t reads tiles t and t+1, issues tile t+3 into the buffer of tile t-1 (last read
   // before the previous barrier) and waits for its own loads of tile t+2, which the barrier then
   // publishes for iteration t+1.
-  for (int t = 0; t < ntiles; ++t) {
+  auto tile_end = [&](int t) {
+    if (t + 3 < ntiles) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __syncthreads();
+  };
+  for (int t = 0; t < tc; ++t) {
+    if (t + 3 < ntiles) issue_tile(t + 3);
+    clean_unit(4 * t + 1, sA, sB, std::integral_constant<int, 1>{});
+    clean_unit(4 * t + 2, sB, sA, std::integral_constant<int, 0>{});
+    clean_unit(4 * t + 3, sA, sB, std::integral_constant<int, 1>{});
+    clean_unit(4 * t + 4, sB, sA, std::integral_constant<int, 0>{});
+    tile_end(t);
+  }
+  for (int t = tc; t < ntiles; ++t) {
     if (t + 3 < ntiles) issue_tile(t + 3);
     unit(4 * t + 1, sA, sB, std::integral_constant<int, 1>{});
     unit(4 * t + 2, sB, sA, std::integral_constant<int, 0>{});
     unit(4 * t + 3, sA, sB, std::integral_constant<int, 1>{});
     unit(4 * t + 4, sB, sA, std::integral_constant<int, 0>{});
-    if (t + 3 < ntiles) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    __syncthreads();
+    tile_end(t);
   }
 
   // ---- epilogue: one IEEE division per row, then products

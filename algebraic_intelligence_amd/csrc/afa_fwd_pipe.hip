@@ -87,10 +87,6 @@ __device__ __forceinline__ float tree16x(const float (&p)[16]) {
   return a[0] + a[2];
 }
 
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9: vmcnt [3:0] and [15:14]; expcnt and
-// lgkmcnt at their no-wait maxima).
-__host__ __device__ constexpr int vm_wait(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-
 template <int D>
 __device__ __forceinline__ int v_swizzle(int r, int c) {
   if constexpr (D == 128) return c ^ ((r & 3) << 1);
@@ -166,8 +162,8 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
         if (lk >= CHD) ks = (const void*)afa_pipe_zero_chunk;
         if (lv >= CHD) vs = (const void*)afa_pipe_zero_chunk;
       }
-      __builtin_amdgcn_global_load_lds(ks, (void*)(kd + (256 * i + wave * 64) * 8), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vs, (void*)(vd + (256 * i + wave * 64) * 8), 16, 0, 0);
+      lds_dma16(ks, kd + (256 * i + wave * 64) * 8);
+      lds_dma16(vs, vd + (256 * i + wave * 64) * 8);
     }
   };
   u32x4_t kf[NK];
@@ -209,8 +205,8 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   // prologue: tiles 0 .. NB-2 in flight; tile 0 resident; S(0) in registers
   const int npro = min(ntiles, NB - 1);
   for (int t = 0; t < npro; ++t) issue_tile(t);
-  if (npro == NB - 1) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * (NB - 2)));
-  else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+  if (npro == NB - 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS * (NB - 2)));
+  else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
   if (ntiles > 0) {
     read_kf(0);
@@ -271,8 +267,8 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   for (int u = 0; u < ntiles; ++u) {
     // own loads of tile u+1 done (those of later tiles may remain), then publish them; the
     // barrier also ends every wave's unit u-1, the last reader of the buffer reused below
-    if (u + 2 < ntiles) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * (NB - 3)));
-    else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    if (u + 2 < ntiles) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS * (NB - 3)));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
     if (u + NB - 1 < ntiles) issue_tile(u + NB - 1);
     if (u & 1) unit(u, sB, sA);
