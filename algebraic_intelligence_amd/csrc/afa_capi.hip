@@ -137,7 +137,8 @@ namespace {
 // ---------------------------------------------------------------------------------- forward
 // Path of an afa_fwd call and the workspace it needs (byte offsets of 256-byte aligned regions):
 //   bf16 / fp16 matrix-core kernels: the fast-rho guard's key bounds (B H ceil(L/64) floats),
-//     then, with rotary tables on the pipelined kernels, the rotated k (B H L D elements);
+//     then, with rotary tables on the pipelined kernels, the rotated k (B H L D elements), then,
+//     when the 128-query kernel splits long key ranges (PipeSplit), its partials and counters;
 //   fp32 matrix-core kernel: the split-K partials when its grid is split;
 //   generic kernel: nothing.
 enum { FWD_GENERIC = 0, FWD_FUSED = 1, FWD_PIPE = 2, FWD_F32 = 3 };
@@ -146,14 +147,16 @@ struct FwdPlan {
   bool wide = false;  // FWD_PIPE at head_dim 64: the 256-query kernel (afa_fwd_d64.hip)
   bool rotk = false;  // FWD_PIPE with rotary tables: k rotated once into the workspace
   int nsplit = 1;     // FWD_F32: key splits
-  size_t kbm = 0, krot = 0, part = 0, total = 0;
+  afa::PipeSplit ks;  // FWD_PIPE 128-query kernel: key split (ks.tiles = 0: none)
+  size_t kbm = 0, krot = 0, part = 0, ks_part = 0, ks_cnt = 0, total = 0;
 };
 
 // mfma_layout: 16-byte aligned q, k, v, out (and tables) with 8-element strides; f32_layout: the
 // fp32 kernel's float4 rows of v and out; in_head_32: K and V rows addressable by 32-bit byte
 // offsets within a head (the pipelined kernels' loads).
+// causal < 0 (workspace queries): the larger of the causal and the non-causal needs.
 FwdPlan fwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, int64_t vlen, bool rotary,
-                 bool mfma_layout, bool f32_layout, bool in_head_32, unsigned flags) {
+                 bool mfma_layout, bool f32_layout, bool in_head_32, unsigned flags, int causal) {
   FwdPlan p;
   if (flags & (AFA_FLAG_GENERIC | AFA_FLAG_EXACT_REF)) return p;
   const bool fused_ok = afa::mfma_fwd_supported(dtype, (int)D);
@@ -172,6 +175,25 @@ FwdPlan fwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, int64_t 
         p.rotk = true;
         p.krot = off;
         off += align256((size_t)(B * H * L * D) * 2);
+      }
+      // the split's counters are cleared by the norm pre-pass, which runs with rotary tables or
+      // under the fast-rho guard
+      if (!p.wide && (rotary || !(flags & AFA_FLAG_EXACT_TAIL))) {
+        if (causal >= 0) {
+          p.ks = afa::pipe_split_plan((int)D, B * H, L, causal != 0, cu_count());
+        } else {
+          const afa::PipeSplit c = afa::pipe_split_plan((int)D, B * H, L, true, cu_count());
+          const afa::PipeSplit n = afa::pipe_split_plan((int)D, B * H, L, false, cu_count());
+          p.ks = c.part_bytes + c.cnt_bytes >= n.part_bytes + n.cnt_bytes ? c : n;
+          p.ks.part_bytes = std::max(c.part_bytes, n.part_bytes);
+          p.ks.cnt_bytes = std::max(c.cnt_bytes, n.cnt_bytes);
+        }
+        if (p.ks.tiles > 0) {
+          p.ks_part = off;
+          off += align256(p.ks.part_bytes);
+          p.ks_cnt = off;
+          off += align256(p.ks.cnt_bytes);
+        }
       }
     } else {
       p.kind = FWD_FUSED;
@@ -237,7 +259,7 @@ size_t afa_fwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t s
                               int rotary) {
   if (fwd_check(dtype, batch, heads, seq_len, head_dim) != AFA_OK) return 0;
   const bool in_head = (seq_len - 1) * head_dim + head_dim < (int64_t(1) << 31);
-  return fwd_plan(dtype, batch, heads, seq_len, head_dim, seq_len, rotary != 0, true, true, in_head, 0).total;
+  return fwd_plan(dtype, batch, heads, seq_len, head_dim, seq_len, rotary != 0, true, true, in_head, 0, -1).total;
 }
 
 int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
@@ -268,7 +290,7 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     return row_stride >= 0 && (seq_len - 1) * row_stride + head_dim < (int64_t(1) << 31);
   };
   const FwdPlan plan = fwd_plan(dtype, batch, heads, seq_len, head_dim, vlen, rot_cos != nullptr, mfma_layout,
-                                f32_layout, in_head_32(st.v[5]) && in_head_32(st.v[8]), flags);
+                                f32_layout, in_head_32(st.v[5]) && in_head_32(st.v[8]), flags, causal ? 1 : 0);
 
   char* ws = (char*)workspace;
   bool owned = false;
@@ -304,10 +326,23 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   hipError_t e = hipSuccess;
   if (plan.kind == FWD_PIPE || plan.kind == FWD_FUSED) {
     float* kbm = (float*)(ws + plan.kbm);
+    int* ks_cnt = nullptr;
+    int nks_cnt = 0;
+    if (plan.ks.tiles > 0) {
+      a.ks_tiles = plan.ks.tiles;
+      a.ks_q0 = plan.ks.q0;
+      a.ks_pmax = plan.ks.pmax;
+      a.ks_items = plan.ks.items;
+      a.ks_part = (float*)(ws + plan.ks_part);
+      a.ks_cnt = ks_cnt = (int*)(ws + plan.ks_cnt);
+      nks_cnt = (int)(plan.ks.cnt_bytes / sizeof(int));
+    }
     if (plan.rotk) {
-      e = afa::krot_launch(dtype, (int)head_dim, a, ws + plan.krot, kbm, s);  // a.k, a.kbm now the rotated k
+      // a.k, a.kbm now the rotated k
+      e = afa::krot_launch(dtype, (int)head_dim, a, ws + plan.krot, kbm, s, ks_cnt, nks_cnt);
     } else if (!exact) {
-      e = afa::rownorm_launch(dtype, k, st.v[3], st.v[4], st.v[5], a.B, a.H, a.L, (int)head_dim, kbm, s);
+      e = afa::rownorm_launch(dtype, k, st.v[3], st.v[4], st.v[5], a.B, a.H, a.L, (int)head_dim, kbm, s, ks_cnt,
+                              nks_cnt);
       a.kbm = kbm;
       a.nkb = (a.L + 63) / 64;
     }

@@ -95,8 +95,9 @@ typedef unsigned short D64Tile[D64_KT * 64];
 // fast-rho guard (fast_rho_safe).
 template <int DT, int D>
 __global__ __launch_bounds__(256) void afa_krot_kernel(const FwdArgs a, unsigned short* y, float* nb2, int nblk,
-                                                      int nwork) {
+                                                      int nwork, int* zero, int nzero) {
   using RL = RowBlockLayout<D>;
+  for (int i = blockIdx.x * 256 + (int)threadIdx.x; i < nzero; i += gridDim.x * 256) zero[i] = 0;
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (int)(threadIdx.x >> 6);  // wave-uniform work item
   if (w >= nwork) return;
@@ -497,26 +498,28 @@ static hipError_t launch_d64(const FwdArgs& a, hipStream_t stream) {
 size_t krot_bytes(const FwdArgs& a, int head_dim) { return (size_t)a.B * a.H * a.L * head_dim * 2; }
 
 template <int D>
-static void krot_launch_d(int dtype, const FwdArgs& a, void* krot, float* nb2, hipStream_t stream) {
+static void krot_launch_d(int dtype, const FwdArgs& a, void* krot, float* nb2, hipStream_t stream, int* zero,
+                          int nzero) {
   const int nblk = (a.L + 63) / 64;
   const int nwork = a.B * a.H * nblk;
   const dim3 grid((unsigned)((nwork + 3) / 4));
   if (dtype == AFA_BF16)
     hipLaunchKernelGGL((afa_krot_kernel<AFA_BF16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2,
-                       nblk, nwork);
+                       nblk, nwork, zero, nzero);
   else
     hipLaunchKernelGGL((afa_krot_kernel<AFA_F16, D>), grid, dim3(256), 0, stream, a, (unsigned short*)krot, nb2,
-                       nblk, nwork);
+                       nblk, nwork, zero, nzero);
 }
 
-hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, float* nb2, hipStream_t stream) {
+hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, float* nb2, hipStream_t stream, int* zero,
+                       int nzero) {
   if (krot == nullptr || nb2 == nullptr) return hipErrorInvalidValue;
   switch (head_dim) {
-    case 32: krot_launch_d<32>(dtype, a, krot, nb2, stream); break;
-    case 48: krot_launch_d<48>(dtype, a, krot, nb2, stream); break;
-    case 64: krot_launch_d<64>(dtype, a, krot, nb2, stream); break;
-    case 96: krot_launch_d<96>(dtype, a, krot, nb2, stream); break;
-    case 128: krot_launch_d<128>(dtype, a, krot, nb2, stream); break;
+    case 32: krot_launch_d<32>(dtype, a, krot, nb2, stream, zero, nzero); break;
+    case 48: krot_launch_d<48>(dtype, a, krot, nb2, stream, zero, nzero); break;
+    case 64: krot_launch_d<64>(dtype, a, krot, nb2, stream, zero, nzero); break;
+    case 96: krot_launch_d<96>(dtype, a, krot, nb2, stream, zero, nzero); break;
+    case 128: krot_launch_d<128>(dtype, a, krot, nb2, stream, zero, nzero); break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();

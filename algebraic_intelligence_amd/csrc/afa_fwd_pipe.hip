@@ -28,6 +28,7 @@
 //     output features are stored.  1/sqrt(D) is a power of two folded into q exactly times an
 //     fp32 factor applied to the score: s = (q 2^-k . k) * (fl(1/sqrt D) 2^k) rounds like the
 //     reference's (q . k) * fl(1/sqrt D).
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -109,9 +110,86 @@ __device__ __attribute__((aligned(16))) unsigned int afa_pipe_zero_chunk[4];
 // SM: 0 = s as formed (q carries 1/sqrt(D) exactly, D = 64);
 //     1 = s = sqrt(2) x evaluated as (rho/sqrt 2)^8 = rho^8/16 (weights and sink carry 1/16);
 //     2 = s = a.s_mult x formed explicitly.
+// Key range of one workgroup: tiles [t0, t1) of its query block, part `part` of `nparts`.
+struct PipePart {
+  int t0 = 0, t1 = 1 << 30, part = 0, nparts = 1;
+};
+
+// 32-key tiles of query block q for the split plan (valid_len = L).
+__device__ __forceinline__ int split_block_tiles(const FwdArgs& a, int q) {
+  return a.causal ? (min(a.L, 128 * (q + 1)) + 31) / 32 : (a.L + 31) / 32;
+}
+
+// Work item of the split grid: the items of one (query block, part) rank are the B * H heads
+// (grouped per XCD as in block_item), ranks run from the last query block down (the longest
+// parts first); a block from ks_q0 on has ceil(tiles / ks_tiles) parts of an even number of tiles
+// each but the last.
+__device__ __forceinline__ void split_item(const FwdArgs& a, int bid, int& bh, int& qblk, PipePart& pp) {
+  const int BH = a.B * a.H;
+  int rank;
+  if ((BH & 7) == 0) {
+    const int hq = BH >> 3, j = bid >> 3;
+    bh = (bid & 7) * hq + j % hq;
+    rank = j / hq;
+  } else {
+    bh = bid % BH;
+    rank = bid / BH;
+  }
+  qblk = 0;
+  pp = PipePart();
+  for (int q = a.nqb - 1; q >= 0; --q) {
+    const int nt = split_block_tiles(a, q);
+    const int np = q < a.ks_q0 ? 1 : (nt + a.ks_tiles - 1) / a.ks_tiles;
+    if (rank < np) {
+      qblk = q;
+      pp.part = rank;
+      pp.nparts = np;
+      pp.t0 = 2 * ((rank * nt) / (2 * np));
+      pp.t1 = rank + 1 == np ? nt : 2 * (((rank + 1) * nt) / (2 * np));
+      break;
+    }
+    rank -= np;
+  }
+}
+
 // LDS tile of the pipelined kernels: 32 keys x the padded head dim.
 template <int DP>
 using PipeTile = unsigned short[32 * DP];
+
+// Direct global -> LDS loads of key tile t (32 keys of K and of V) of one head into ring buffer
+// t % NB: slot s = tid + 256 i covers row s / CH, physical chunk s % CH; K chunk c of row r goes to
+// c ^ (r & 7), V chunk c to v_swizzle; rows past L read row L - 1 (finite data, masked keys).
+template <int D>
+__device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padded_dim(D)>* lds_k,
+                                                PipeTile<padded_dim(D)>* lds_v, const unsigned short* kp,
+                                                const unsigned short* vp, int t) {
+  constexpr int DP = padded_dim(D);
+  constexpr int KT = 32;
+  constexpr int NB = PipeShape<DP>::NB;
+  constexpr int CH = DP / 8;
+  constexpr int CHD = D / 8;
+  constexpr int LPT = KT * CH / 256;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  unsigned short* kd = &lds_k[t % NB][0];
+  unsigned short* vd = &lds_v[t % NB][0];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int s = tid + 256 * i, r = s / CH, pc = s % CH;
+    const int key = min(t * KT + r, a.L - 1);
+    const int lk = pc ^ (r & 7), lv = v_swizzle<DP>(r, pc);
+    // byte offsets within the head fit 32 bits (checked by the caller): a uniform base plus a
+    // 32-bit lane offset per load
+    const void* ks = (const void*)((const char*)kp + (uint32_t)(key * (int)a.k_l + lk * 8) * 2u);
+    const void* vs = (const void*)((const char*)vp + (uint32_t)(key * (int)a.v_l + lv * 8) * 2u);
+    if constexpr (CHD < CH) {
+      if (lk >= CHD) ks = (const void*)afa_pipe_zero_chunk;
+      if (lv >= CHD) vs = (const void*)afa_pipe_zero_chunk;
+    }
+    lds_dma16(ks, kd + (256 * i + wave * 64) * 8);
+    lds_dma16(vs, vd + (256 * i + wave * 64) * 8);
+  }
+}
 
 // Tile loop and epilogue of afa_fwd_pipe_kernel for one form of rho^8: FAST, the branch-free
 // form (the wave's scores are all within the fast-rho bound), else the two-branch form.  The
@@ -120,7 +198,7 @@ using PipeTile = unsigned short[32 * DP];
 template <int D, int DT, bool FAST, int SM>
 __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(D)>* lds_k,
                                           PipeTile<padded_dim(D)>* lds_v, const u32x4_t (&qf)[padded_dim(D) / 16],
-                                          int bh, int qblk) {
+                                          int bh, int qblk, const PipePart& pp) {
   constexpr int DP = padded_dim(D);      // LDS row and MFMA width
   constexpr int KT = 32;                 // keys per tile = one unit
   constexpr int NB = PipeShape<DP>::NB;
@@ -139,33 +217,15 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   const int q0_wg = qblk * 128, q0_w = q0_wg + wave * 32;
   const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 128)) : vlen;
   const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
+  // this workgroup's key tiles [t_lo, t_hi): its part of the block's tiles (all of them unsplit)
   const int ntiles = (kend_wg + KT - 1) / KT;
-  const int U = q0_w < L ? (kend_w + KT - 1) / KT : 0;  // units of this wave
+  const int t_hi = min(pp.t1, ntiles), t_lo = min(pp.t0, t_hi);
+  const int U = min(q0_w < L ? (kend_w + KT - 1) / KT : 0, t_hi);  // end of this wave's units
   const int qi = q0_w + l32;
   const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
 
-  // direct loads: slot s = tid + 256 i covers row s / CH, physical chunk s % CH
-  auto issue_tile = [&](int t) {
-    unsigned short* kd = &lds_k[t % NB][0];
-    unsigned short* vd = &lds_v[t % NB][0];
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int s = tid + 256 * i, r = s / CH, pc = s % CH;
-      const int key = min(t * KT + r, L - 1);  // rows past L: finite data, masked
-      const int lk = pc ^ (r & 7), lv = v_swizzle<DP>(r, pc);
-      // byte offsets within the head fit 32 bits (checked by the caller): a uniform base plus a
-      // 32-bit lane offset per load
-      const void* ks = (const void*)((const char*)kp + (uint32_t)(key * (int)a.k_l + lk * 8) * 2u);
-      const void* vs = (const void*)((const char*)vp + (uint32_t)(key * (int)a.v_l + lv * 8) * 2u);
-      if constexpr (CHD < CH) {
-        if (lk >= CHD) ks = (const void*)afa_pipe_zero_chunk;
-        if (lv >= CHD) vs = (const void*)afa_pipe_zero_chunk;
-      }
-      lds_dma16(ks, kd + (256 * i + wave * 64) * 8);
-      lds_dma16(vs, vd + (256 * i + wave * 64) * 8);
-    }
-  };
+  auto issue_tile = [&](int t) { pipe_issue_tile<D>(a, lds_k, lds_v, kp, vp, t); };
   u32x4_t kf[NK];
   u32x4_t vf[NDB][2];
   auto read_kf = [&](int u) {
@@ -202,14 +262,14 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   float rowsum = 0.f;
   f32x16_t sA, sB;
 
-  // prologue: tiles 0 .. NB-2 in flight; tile 0 resident; S(0) in registers
-  const int npro = min(ntiles, NB - 1);
-  for (int t = 0; t < npro; ++t) issue_tile(t);
+  // prologue: tiles t_lo .. t_lo+NB-2 in flight (issued by the kernel before its q loads); tile
+  // t_lo resident; S(t_lo) in registers (t_lo is even, so S(u) is in sA for even u as in the loop)
+  const int npro = min(t_hi - t_lo, NB - 1);
   if (npro == NB - 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS * (NB - 2)));
   else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
-  if (ntiles > 0) {
-    read_kf(0);
+  if (t_lo < t_hi) {
+    read_kf(t_lo);
 #pragma unroll
     for (int e = 0; e < 16; ++e) sA[e] = 0.f;
 #pragma unroll
@@ -264,15 +324,61 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
       for (int db = 0; db < NDB; ++db) o[db] = mma16<DT>(vf[db][kk], pk[kk], o[db]);
   };
 
-  for (int u = 0; u < ntiles; ++u) {
+  for (int u = t_lo; u < t_hi; ++u) {
     // own loads of tile u+1 done (those of later tiles may remain), then publish them; the
     // barrier also ends every wave's unit u-1, the last reader of the buffer reused below
-    if (u + 2 < ntiles) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS * (NB - 3)));
+    if (u + 2 < t_hi) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS * (NB - 3)));
     else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
-    if (u + NB - 1 < ntiles) issue_tile(u + NB - 1);
+    if (u + NB - 1 < t_hi) issue_tile(u + NB - 1);
     if (u & 1) unit(u, sB, sA);
     else unit(u, sA, sB);
+  }
+
+  // key split: every part stores its fp32 partial numerators and row sums, then counts itself
+  // in; the last part of the block to arrive adds all parts' partials (in part order, so that
+  // the sum does not depend on which part finished last) and stores the block.  The partials go
+  // through device-scope relaxed atomic stores and loads (written through to, and read from,
+  // the point where every XCD sees them), so no cache-wide write-back or invalidate is needed:
+  // a part's stores are complete (vmcnt 0) before its count, and the last part reads after its
+  // own count.
+  if (pp.nparts > 1) {
+    __shared__ int ks_last;
+    // a part's partial, lane-major so that every store and load instruction covers 256
+    // contiguous bytes: per wave, NDB * 16 accumulator values, then the row sum, each for the 64
+    // lanes (the last part's lanes hold the same rows and features as every other part's)
+    constexpr int NV = NDB * 16 + 1;
+    constexpr int PSTRIDE = 4 * NV * 64;  // floats per part
+    const int blk = bh * (a.nqb - a.ks_q0) + (qblk - a.ks_q0);
+    float* parts = a.ks_part + (size_t)blk * a.ks_pmax * PSTRIDE + wave * NV * 64 + lane;
+    float* mine = parts + (size_t)pp.part * PSTRIDE;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        __hip_atomic_store(mine + (db * 16 + e) * 64, o[db][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(mine + (NV - 1) * 64, rowsum + __shfl_xor(rowsum, 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __syncthreads();
+    if (tid == 0) ks_last = atomicAdd(a.ks_cnt + blk, 1) == pp.nparts - 1;
+    __syncthreads();
+    if (!ks_last) return;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+    float total = 0.f;
+    for (int p2 = 0; p2 < pp.nparts; ++p2) {
+      const float* part = parts + (size_t)p2 * PSTRIDE;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          o[db][e] += __hip_atomic_load(part + (db * 16 + e) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      total += __hip_atomic_load(part + (NV - 1) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    rowsum = g == 0 ? total : 0.f;
   }
 
   // epilogue
@@ -316,7 +422,9 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
   __shared__ __attribute__((aligned(16))) PipeTile<DP> lds_v[NB];
 
   int bh, qblk;
-  block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
+  PipePart pp;
+  if (a.ks_tiles == 0) block_item(blockIdx.x, a.B * a.H, a.nqb, a.causal, bh, qblk);
+  else split_item(a, (int)blockIdx.x, bh, qblk, pp);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -327,6 +435,16 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
   const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 128)) : vlen;
   const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
   const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
+
+  // the first tiles of this workgroup's key range go out before the q loads, so that their
+  // memory latencies overlap (pipe_body waits for them)
+  {
+    const int ntiles = (kend_wg + KT - 1) / KT;
+    const int t_hi = min(pp.t1, ntiles), t_lo = min(pp.t0, t_hi);
+    const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
+    const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
+    for (int t = t_lo; t < t_lo + min(t_hi - t_lo, NB - 1); ++t) pipe_issue_tile<D>(a, lds_k, lds_v, kp, vp, t);
+  }
 
   // q fragments (B operand of S^T = K Q^T): query q0_w + l32, features kc*16 + 8g .. +7
   const int qi = q0_w + l32;
@@ -353,15 +471,15 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
                          wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim);
   }
 
-  if (fast) pipe_body<D, DT, true, SM>(a, lds_k, lds_v, qf, bh, qblk);
-  else pipe_body<D, DT, false, SM>(a, lds_k, lds_v, qf, bh, qblk);
+  if (fast) pipe_body<D, DT, true, SM>(a, lds_k, lds_v, qf, bh, qblk, pp);
+  else pipe_body<D, DT, false, SM>(a, lds_k, lds_v, qf, bh, qblk, pp);
 }
 
 namespace {
 
 template <int D, int DT, bool EXACT, int SM>
 hipError_t launch_pipe(const FwdArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)(a.B * a.H * a.nqb));
+  const dim3 grid((unsigned)(a.ks_tiles > 0 ? a.ks_items : a.B * a.H * a.nqb));
   if (a.rc != nullptr)
     hipLaunchKernelGGL((afa_fwd_pipe_kernel<D, DT, EXACT, SM, true>), grid, dim3(256), 0, st, a);
   else
@@ -370,6 +488,38 @@ hipError_t launch_pipe(const FwdArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+
+PipeSplit pipe_split_plan(int head_dim, int64_t BH, int64_t L, bool causal, int cus) {
+  PipeSplit ps;
+  const int DP = head_dim <= 64 ? 64 : 128;
+  const int64_t slots = (int64_t)cus * (DP == 128 ? PipeShape<128>::WAVES_PER_EU : PipeShape<64>::WAVES_PER_EU);
+  const int64_t nqb = (L + 127) / 128;
+  auto tiles = [&](int64_t q) { return causal ? (std::min(L, 128 * (q + 1)) + 31) / 32 : (L + 31) / 32; };
+  int64_t total = 0;
+  for (int64_t q = 0; q < nqb; ++q) total += tiles(q);
+  total *= BH;
+  // parts of about the balanced load per workgroup slot, at least 16 tiles (512 keys) each, and
+  // the partials (fp32 rows of every part of every split block) within 48 MiB
+  for (int64_t T = std::max<int64_t>((total + slots - 1) / slots, 16); T <= tiles(nqb - 1); T *= 2) {
+    T = (T + 1) & ~(int64_t)1;
+    if (tiles(nqb - 1) * 4 <= T * 5) return ps;  // the longest block is within 25% of a part
+    int64_t q0 = 0;
+    while (tiles(q0) <= T) ++q0;
+    const int64_t pmax = (tiles(nqb - 1) + T - 1) / T;
+    const size_t part_bytes = (size_t)(BH * (nqb - q0) * pmax) * 4 * (DP / 2 + 1) * 64 * sizeof(float);
+    if (part_bytes > ((size_t)48 << 20)) continue;
+    int64_t ranks = 0;
+    for (int64_t q = 0; q < nqb; ++q) ranks += q < q0 ? 1 : (tiles(q) + T - 1) / T;
+    ps.tiles = (int)T;
+    ps.q0 = (int)q0;
+    ps.pmax = (int)pmax;
+    ps.items = (int)(ranks * BH);
+    ps.part_bytes = part_bytes;
+    ps.cnt_bytes = (size_t)(BH * (nqb - q0)) * sizeof(int);
+    return ps;
+  }
+  return ps;
+}
 
 bool pipe_fwd_supported(int dtype, int head_dim) {
   return (dtype == AFA_BF16 || dtype == AFA_F16) &&

@@ -32,6 +32,29 @@ struct FwdArgs {
   const float* kbm;
   int nkb;
   float nb_lim;
+  // key split of the pipelined kernel (PipeSplit below): query blocks from ks_q0 on are processed
+  // in parts of up to ks_tiles 32-key tiles by ks_items workgroups in all; every part writes its
+  // fp32 partial numerators and row sums to ks_part and counts itself in ks_cnt (one int per
+  // split block, zero on entry), and the last part of a block to arrive adds the others' partials
+  // and stores the block.  ks_tiles = 0: no split.
+  int ks_tiles;
+  int ks_q0;
+  int ks_pmax;
+  int ks_items;
+  float* ks_part;
+  int* ks_cnt;
+};
+
+// Key split of the pipelined kernel for one shape: causal rows near the end of a long sequence,
+// or every row of a grid with fewer 128-query blocks than workgroup slots, would otherwise leave
+// one workgroup's key loop as the critical path of the whole call.  Planned for valid_len = L;
+// with a shorter valid_len some parts have no keys and contribute zero partials.
+struct PipeSplit {
+  int tiles = 0;       // 32-key tiles per part (0: no split)
+  int q0 = 0;          // first split query block
+  int pmax = 1;        // parts of the last query block (the most of any block)
+  int items = 0;       // workgroups of the launch
+  size_t part_bytes = 0, cnt_bytes = 0;
 };
 
 // Generic forward / backward (afa_generic.hip).
@@ -74,14 +97,16 @@ hipError_t mfma_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipSt
 // (krot_bytes bytes, contiguous B, H, L, D); a's k then points at it, and a's key bounds at nb2
 // (B H ceil(L/64) floats), which the same launch fills from the rotated rows.
 size_t krot_bytes(const FwdArgs& a, int head_dim);
-hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, float* nb2, hipStream_t stream);
+hipError_t krot_launch(int dtype, int head_dim, FwdArgs& a, void* krot, float* nb2, hipStream_t stream,
+                       int* zero = nullptr, int nzero = 0);
 // Bound of the fast-rho guard: kFastRhoMaxScore^2 / (score / MFMA-output)^2, less a 5% margin for
 // the rounding of the norms and of the rotated operands.
 float fast_rho_lim(double score_per_output);
 // Largest squared row norm of each 64-row block of x (bf16 / fp16; rows of head_dim elements,
 // 16-byte aligned, element strides per (b, h, l)) into nb2[bh * ceil(L/64) + block].
+// Both norm pre-passes also clear the `nzero` ints at `zero` (the key split's counters; nullptr: none).
 hipError_t rownorm_launch(int dtype, const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
-                          int head_dim, float* nb2, hipStream_t stream);
+                          int head_dim, float* nb2, hipStream_t stream, int* zero = nullptr, int nzero = 0);
 // Software-pipelined head_dim-64 kernel (afa_fwd_d64.hip); 256 queries per workgroup.  q is
 // rotated at load when a.rc is set; k must arrive rotated (krot_launch).
 hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);
@@ -89,6 +114,9 @@ hipError_t d64_fwd_launch(int dtype, FwdArgs a, bool exact, hipStream_t stream);
 // 128 (rows zero-padded to 64 or 128 in LDS), 128 queries per workgroup; q is rotated at load
 // when a.rc is set, k must arrive rotated.
 bool pipe_fwd_supported(int dtype, int head_dim);
+// Key split for B * H heads of L queries on `cus` compute units (tiles = 0 when none pays off).
+PipeSplit pipe_split_plan(int head_dim, int64_t BH, int64_t L, bool causal, int cus);
+// a.ks_*: the split (ks_tiles = 0 for none; the counters cleared by a pre-pass of the same call).
 hipError_t pipe_fwd_launch(int dtype, int head_dim, FwdArgs a, bool exact, hipStream_t stream);
 
 // fp32 forward on the fp32 MFMA (afa_fwd_f32.hip): head_dim 32/64/128, V and out rows 16-byte

@@ -18,8 +18,9 @@ namespace afa {
 template <int DT, int D>
 __global__ __launch_bounds__(256) void afa_rownorm_kernel(const unsigned short* x, int64_t sb, int64_t sh,
                                                          int64_t sl, int H, int L, int nblk, int nwork,
-                                                         float* nb2) {
+                                                         float* nb2, int* zero, int nzero) {
   using RL = RowBlockLayout<D>;
+  for (int i = blockIdx.x * 256 + (int)threadIdx.x; i < nzero; i += gridDim.x * 256) zero[i] = 0;
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (int)(threadIdx.x >> 6);  // wave-uniform work item
   if (w >= nwork) return;
@@ -43,23 +44,23 @@ __global__ __launch_bounds__(256) void afa_rownorm_kernel(const unsigned short* 
 
 template <int DT, int D>
 static void rownorm_launch_d(const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, float* nb2,
-                             hipStream_t stream) {
+                             hipStream_t stream, int* zero, int nzero) {
   const int nblk = (L + 63) / 64;
   const int nwork = B * H * nblk;
   hipLaunchKernelGGL((afa_rownorm_kernel<DT, D>), dim3((unsigned)((nwork + 3) / 4)), dim3(256), 0, stream,
-                     (const unsigned short*)x, sb, sh, sl, H, L, nblk, nwork, nb2);
+                     (const unsigned short*)x, sb, sh, sl, H, L, nblk, nwork, nb2, zero, nzero);
 }
 
 template <int DT>
 static hipError_t rownorm_launch_dt(const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
-                                    int head_dim, float* nb2, hipStream_t stream) {
+                                    int head_dim, float* nb2, hipStream_t stream, int* zero, int nzero) {
   switch (head_dim) {
-    case 32: rownorm_launch_d<DT, 32>(x, sb, sh, sl, B, H, L, nb2, stream); break;
-    case 48: rownorm_launch_d<DT, 48>(x, sb, sh, sl, B, H, L, nb2, stream); break;
-    case 64: rownorm_launch_d<DT, 64>(x, sb, sh, sl, B, H, L, nb2, stream); break;
-    case 96: rownorm_launch_d<DT, 96>(x, sb, sh, sl, B, H, L, nb2, stream); break;
-    case 128: rownorm_launch_d<DT, 128>(x, sb, sh, sl, B, H, L, nb2, stream); break;
-    case 256: rownorm_launch_d<DT, 256>(x, sb, sh, sl, B, H, L, nb2, stream); break;
+    case 32: rownorm_launch_d<DT, 32>(x, sb, sh, sl, B, H, L, nb2, stream, zero, nzero); break;
+    case 48: rownorm_launch_d<DT, 48>(x, sb, sh, sl, B, H, L, nb2, stream, zero, nzero); break;
+    case 64: rownorm_launch_d<DT, 64>(x, sb, sh, sl, B, H, L, nb2, stream, zero, nzero); break;
+    case 96: rownorm_launch_d<DT, 96>(x, sb, sh, sl, B, H, L, nb2, stream, zero, nzero); break;
+    case 128: rownorm_launch_d<DT, 128>(x, sb, sh, sl, B, H, L, nb2, stream, zero, nzero); break;
+    case 256: rownorm_launch_d<DT, 256>(x, sb, sh, sl, B, H, L, nb2, stream, zero, nzero); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -71,10 +72,10 @@ float fast_rho_lim(double score_per_output) {
 }
 
 hipError_t rownorm_launch(int dtype, const void* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L,
-                          int head_dim, float* nb2, hipStream_t stream) {
+                          int head_dim, float* nb2, hipStream_t stream, int* zero, int nzero) {
   if (x == nullptr || nb2 == nullptr) return hipErrorInvalidValue;
-  if (dtype == AFA_BF16) return rownorm_launch_dt<AFA_BF16>(x, sb, sh, sl, B, H, L, head_dim, nb2, stream);
-  if (dtype == AFA_F16) return rownorm_launch_dt<AFA_F16>(x, sb, sh, sl, B, H, L, head_dim, nb2, stream);
+  if (dtype == AFA_BF16) return rownorm_launch_dt<AFA_BF16>(x, sb, sh, sl, B, H, L, head_dim, nb2, stream, zero, nzero);
+  if (dtype == AFA_F16) return rownorm_launch_dt<AFA_F16>(x, sb, sh, sl, B, H, L, head_dim, nb2, stream, zero, nzero);
   return hipErrorInvalidValue;
 }
 

@@ -127,6 +127,40 @@ def test_c5_backward_full_length(c5):
             assert e <= 1e-2, name
 
 
+# ----------------------------------------------------------------------------------- key split
+@pytest.mark.parametrize("shape,causal,valid,dt,rotary", [
+    ((1, 8, 2048, 64), True, None, torch.bfloat16, False),
+    ((1, 8, 2048, 64), False, 1500, torch.bfloat16, False),
+    ((2, 4, 2048, 128), True, None, torch.bfloat16, True),
+    ((1, 4, 2048, 96), True, 1900, torch.float16, False),
+    ((1, 2, 1536, 32), False, None, torch.bfloat16, True),
+])
+def test_key_split_matches_contract(shape, causal, valid, dt, rotary):
+    """Grids with few 128-query blocks split the long key ranges over several workgroups, whose
+    fp32 partials the last one to finish adds up.  Such a call reserves workspace beyond the
+    guard's key bounds (B H ceil(L/64) floats, and the rotated k with rotary tables); its output
+    and denominator match the C restatement of the contract as unsplit calls do, also where
+    valid_len leaves some parts without keys."""
+    B, H, L, D = shape
+    q, k, v = make_qkv(shape, dt, seed=61 + D, scale=0.5)
+    rot = A.build_cayley_rotary_matrix(D, L) if rotary else None
+    ws = _lib.lib().afa_fwd_workspace_size(_lib.dtype_code(dt), B, H, L, D, int(rotary))
+    base = -(-B * H * ((L + 63) // 64) * 4 // 256) * 256
+    if rotary:
+        base += -(-B * H * L * D * 2 // 256) * 256
+    assert ws > base, "no key split planned for this shape"
+    out, den = _fwd(q, k, v, causal=causal, valid=valid, rotary=rot)
+    c_out, c_den = oracle_contract(q, k, v, 0.5, causal, valid, rotary=rot)
+    e, e_d = normwise(to_f64(out), c_out), normwise(to_f64(den), c_den)
+    print(f"{shape} causal={causal} valid={valid} {dt} rotary={rotary}: workspace {ws} B, vs contract {e:.2e}, "
+          f"denominator {e_d:.2e}")
+    assert np.isfinite(to_f64(out)).all()
+    assert e <= _ulp_tol(dt) and e_d <= 1e-4
+    # the parts are added in part order whichever finishes last: calls are bit for bit repeatable
+    out2, den2 = _fwd(q, k, v, causal=causal, valid=valid, rotary=rot)
+    assert torch.equal(out, out2) and torch.equal(den, den2)
+
+
 # ----------------------------------------------------------------------------------- tiled entry point
 @pytest.mark.parametrize("dt,causal,valid", [(torch.float32, False, 200), (torch.bfloat16, True, 300),
                                              (torch.bfloat16, False, None), (torch.float16, True, 129)])
