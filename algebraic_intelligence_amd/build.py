@@ -70,7 +70,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
                            "; ".join(f"{k} in {', '.join(v)}" for k, v in sorted(dup.items())))
     # --no-undefined: a kernel whose host stub was not emitted must fail here, not at load time
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", *objs,
-           "-L/opt/rocm/lib", "-lhipblaslt", "-o", LIB + ".tmp"]
+           "-o", LIB + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

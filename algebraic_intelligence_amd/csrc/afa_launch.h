@@ -193,4 +193,27 @@ size_t oace_mfma_workspace(int dtype, const OaceArgs& a);
 hipError_t oace_linear_fwd_mfma(int dtype, const OaceArgs& a, void* rows, void* ws, hipStream_t st);
 hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, void* ws, hipStream_t st);
 
+// MFMA GEMM of the OACE backward (oace_bwd_gemm.hip): D[n][m] = sum_k A[m][k] B[n][k] in the
+// element type at out[n * ldo + m], fp32 accumulation.  An operand is row-contiguous (mc:
+// element (r, k) at p[k * ld + r]) or contraction-contiguous (element (r, k) at p[r * ld + k]).
+struct OaceGemm {
+  const void* a;
+  int64_t lda;
+  bool a_mc;
+  int64_t m;
+  const void* b;
+  int64_t ldb;
+  bool b_mc;
+  int64_t n;
+  int64_t k;
+  void* out;
+  int64_t ldo;
+};
+bool oace_gemm_fits(const OaceGemm& g);
+// Contraction parts for about `wgs` workgroups (1: no split); parts > 1 need part_bytes of fp32
+// partials, added in part order by a second kernel (row-contiguous A, contiguous B only).
+int oace_gemm_parts(const OaceGemm& g, int wgs);
+size_t oace_gemm_part_bytes(const OaceGemm& g, int parts);
+hipError_t oace_gemm(int dtype, const OaceGemm& g, int parts, float* part, hipStream_t st);
+
 }  // namespace afa

@@ -10,7 +10,7 @@
 // a second sweep costs less than the Gram product whenever rows < d_model, the case of the
 // reference's own benchmark (512 x 768).  The backward recomputes z once:
 //   MODE_DZ:    dz = tau c (r bracket - radial x), stored as the element type (rows, V padded)
-// and hands dh = dz W^T and dW = h^T dz to hipBLASLt (plain GEMMs).
+// and forms dh = dz W^T and dW = h^T dz with the MFMA GEMMs of oace_bwd_gemm.hip.
 //
 // GEMM tile: z^T = W^T h^T over a 256 (vocabulary) x 128 (rows) tile per workgroup, four waves of
 // 64 x 128, each a 2 x 4 grid of 32x32x16 MFMA blocks whose accumulator lanes hold one row and 16
@@ -20,12 +20,8 @@
 // of one vocabulary block are dispatched consecutively on one XCD (they share its W tile in L2).
 // W is used as W^T (vocab, d_model) with d_model contiguous: a tied embedding already is; the
 // (d_model, vocab) output head is transposed once per call into the workspace.
-#include <map>
-#include <mutex>
-#include <tuple>
+#include <algorithm>
 #include <type_traits>
-
-#include <hipblaslt/hipblaslt.h>
 
 #include "oace_common.h"
 
@@ -436,17 +432,6 @@ __global__ __launch_bounds__(256) void oace_mfma_rows_kernel(const float* part, 
   }
 }
 
-// dh = sum of the split-K partials (fixed order), rounded once to the element type.
-template <int DT>
-__global__ __launch_bounds__(256) void oace_mfma_splitk_sum_kernel(const float* part, int parts, int64_t n,
-                                                                   unsigned short* out) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    float s = 0.f;
-    for (int p = 0; p < parts; ++p) s += part[p * n + i];
-    Elem<DT>::store(out, i, s);
-  }
-}
-
 // ------------------------------------------------------------------------------ host side
 namespace {
 
@@ -454,11 +439,7 @@ int64_t nvt_of(int64_t V) { return (V + TV - 1) / TV; }
 int64_t nnt_of(int64_t N) { return (N + TN - 1) / TN; }
 int64_t ldz_of(int64_t V) { return (V + 63) / 64 * 64; }
 size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
-constexpr size_t BLAS_WS = (size_t)64 << 20;
-
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
-int dh_splits(const OaceArgs& a);
 
 // The forward keeps the fp32 logits (rows x padded vocabulary) when they take at most this many
 // bytes -- the reference benchmark's 512 x 50257 take 103 MB, which the 256 MB Infinity Cache
@@ -469,8 +450,17 @@ bool z_cached(const OaceArgs& a) {
   return !(a.flags & OACE_FLAG_RECOMPUTE_Z) && (size_t)a.N * ldz_of(a.V) * sizeof(float) <= ZC_MAX_BYTES;
 }
 
+// dh (N, d) = dz W^T as D[n][m] = sum_v W^T[v][m] dz[n][v]: A = W^T row-contiguous over the
+// model features, B = dz contraction-contiguous.  Its vocabulary contraction is split for this
+// many workgroups: a constant, so that the summation order, and the result, do not depend on
+// the device.
+constexpr int DH_WGS = 256;
+OaceGemm dh_gemm(const OaceArgs& a, const unsigned short* wt, int64_t ldwt, const unsigned short* dz) {
+  return OaceGemm{wt, ldwt, true, a.d, dz, ldz_of(a.V), false, a.N, a.V, a.dh, a.d};
+}
+
 struct Layout {
-  size_t wt, zc, part, dz, dhp, blas, total;
+  size_t wt, zc, part, dz, dhp, total;
 };
 Layout layout_of(const OaceArgs& a) {
   Layout l;
@@ -478,10 +468,9 @@ Layout layout_of(const OaceArgs& a) {
   l.zc = z_cached(a) ? al((size_t)a.N * ldz_of(a.V) * sizeof(float)) : 0;
   l.part = al((size_t)nvt_of(a.V) * a.N * 4 * sizeof(float));
   l.dz = al((size_t)a.N * ldz_of(a.V) * 2);
-  const int s = dh_splits(a);
-  l.dhp = s > 1 ? al((size_t)(s + 1) * a.d * a.N * sizeof(float)) : 0;  // split-K partials of dh
-  l.blas = BLAS_WS;
-  l.total = l.wt + l.zc + std::max(l.part, l.dz + l.dhp + l.blas);
+  const OaceGemm gh = dh_gemm(a, nullptr, a.d, nullptr);
+  l.dhp = al(oace_gemm_part_bytes(gh, oace_gemm_parts(gh, DH_WGS)));  // split-K partials of dh
+  l.total = l.wt + l.zc + std::max(l.part, l.dz + l.dhp);
   return l;
 }
 
@@ -526,181 +515,15 @@ hipError_t launch_gemm_dt(int dtype, const GemmArgs& g, hipStream_t st) {
   return dtype == AFA_BF16 ? launch_gemm<AFA_BF16, MODE>(g, st) : launch_gemm<AFA_F16, MODE>(g, st);
 }
 
-// ---- hipBLASLt for the two plain GEMMs of the backward (one handle per device, created once).
-hipblasLtHandle_t blas_handle() {
-  static std::mutex m;
-  static hipblasLtHandle_t handles[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(m);
-  if (handles[dev] == nullptr && hipblasLtCreate(&handles[dev]) != HIPBLAS_STATUS_SUCCESS) handles[dev] = nullptr;
-  return handles[dev];
-}
-
-// Column-major D (m x n, ldd) = op(A) op(B), k the contraction; A stored (ta ? k x m : m x k) with
-// lda, B stored (tb ? n x k : k x n) with ldb; fp32 accumulation; D in the element type, or fp32
-// when d_f32.  batch > 1: strided batches (element strides sa, sb, sd).
-struct BlasGemm {
-  bool ta, tb;
-  int64_t m, n, k;
-  const void* A;
-  int64_t lda, sa;
-  const void* B;
-  int64_t ldb, sb;
-  void* D;
-  int64_t ldd, sd;
-  bool d_f32;
-  int batch;
-};
-
-// The heuristic's first choice can be far from the best kernel for these shapes (a small output
-// with a long contraction, or the reverse), so the first call for a shape times the heuristic's
-// top candidates once on the real operands and keeps the fastest (per device and shape).  Under
-// stream capture no timing is possible and the first candidate is used.
-constexpr int MAX_ALGOS = 8;
-struct AlgoKey {
-  int dev, dtype;
-  bool ta, tb, d_f32;
-  int batch;
-  int64_t m, n, k, lda, ldb, ldd, sa, sb, sd;
-  bool operator<(const AlgoKey& o) const {
-    return std::tie(dev, dtype, ta, tb, d_f32, batch, m, n, k, lda, ldb, ldd, sa, sb, sd) <
-           std::tie(o.dev, o.dtype, o.ta, o.tb, o.d_f32, o.batch, o.m, o.n, o.k, o.lda, o.ldb, o.ldd, o.sa, o.sb, o.sd);
-  }
-};
-std::mutex& algo_mutex() {
-  static std::mutex m;
-  return m;
-}
-std::map<AlgoKey, hipblasLtMatmulAlgo_t>& algo_cache() {
-  static std::map<AlgoKey, hipblasLtMatmulAlgo_t> c;
-  return c;
-}
-
-int tune(hipblasLtHandle_t h, hipblasLtMatmulDesc_t desc, hipblasLtMatrixLayout_t la, hipblasLtMatrixLayout_t lb,
-         hipblasLtMatrixLayout_t ld, const BlasGemm& g, const hipblasLtMatmulHeuristicResult_t* res, int found,
-         void* ws, size_t wsb, hipStream_t st) {
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (found < 2 || hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return 0;
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess) return 0;
-  if (hipEventCreate(&e1) != hipSuccess) {
-    (void)hipEventDestroy(e0);
-    return 0;
-  }
-  const float alpha = 1.f, beta = 0.f;
-  int best = 0;
-  float best_ms = 3.4e38f;
-  for (int i = 0; i < found; ++i) {
-    if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > wsb) continue;
-    // one untimed run (first-use costs), then one timed run
-    if (hipblasLtMatmul(h, desc, &alpha, g.A, la, g.B, lb, &beta, g.D, ld, g.D, ld, &res[i].algo, ws, wsb, st) !=
-        HIPBLAS_STATUS_SUCCESS)
-      continue;
-    float ms = 0.f;
-    if (hipEventRecord(e0, st) != hipSuccess ||
-        hipblasLtMatmul(h, desc, &alpha, g.A, la, g.B, lb, &beta, g.D, ld, g.D, ld, &res[i].algo, ws, wsb, st) !=
-            HIPBLAS_STATUS_SUCCESS ||
-        hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
-        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
-      continue;
-    if (ms < best_ms) {
-      best_ms = ms;
-      best = i;
-    }
-  }
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  (void)hipGetLastError();
-  return best;
-}
-
-hipError_t blas_gemm(int dtype, const BlasGemm& g, void* ws, size_t wsb, hipStream_t st) {
-  hipblasLtHandle_t h = blas_handle();
-  if (h == nullptr) return hipErrorNotInitialized;
-  const hipDataType t = dtype == AFA_BF16 ? HIP_R_16BF : HIP_R_16F;
-  const hipDataType td = g.d_f32 ? HIP_R_32F : t;
-  hipblasLtMatmulDesc_t desc = nullptr;
-  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
-  hipblasLtMatmulPreference_t pref = nullptr;
-  hipError_t err = hipErrorNotSupported;
-  const hipblasOperation_t opa = g.ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = g.tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-  const uint64_t wsz = wsb;
-  const int32_t bc = g.batch;
-  hipblasLtMatmulHeuristicResult_t res[MAX_ALGOS];
-  int found = 0;
-  const float alpha = 1.f, beta = 0.f;
-  auto batched = [&](hipblasLtMatrixLayout_t l, int64_t stride) {
-    return hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)) ==
-               HIPBLAS_STATUS_SUCCESS &&
-           hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &stride,
-                                             sizeof(stride)) == HIPBLAS_STATUS_SUCCESS;
-  };
-  if (hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) goto done;
-  if (hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(int32_t)) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(int32_t)) != HIPBLAS_STATUS_SUCCESS)
-    goto done;
-  if (hipblasLtMatrixLayoutCreate(&la, t, g.ta ? g.k : g.m, g.ta ? g.m : g.k, g.lda) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&lb, t, g.tb ? g.n : g.k, g.tb ? g.k : g.n, g.ldb) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&ld, td, g.m, g.n, g.ldd) != HIPBLAS_STATUS_SUCCESS)
-    goto done;
-  if (g.batch > 1 && !(batched(la, g.sa) && batched(lb, g.sb) && batched(ld, g.sd))) goto done;
-  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof(wsz)) !=
-          HIPBLAS_STATUS_SUCCESS)
-    goto done;
-  {
-    const AlgoKey key = {0, dtype, g.ta, g.tb, g.d_f32, g.batch, g.m, g.n, g.k, g.lda, g.ldb, g.ldd, g.sa, g.sb, g.sd};
-    AlgoKey k2 = key;
-    (void)hipGetDevice(&k2.dev);
-    const hipblasLtMatmulAlgo_t* algo = nullptr;
-    hipblasLtMatmulAlgo_t chosen;
-    {
-      std::lock_guard<std::mutex> lock(algo_mutex());
-      auto it = algo_cache().find(k2);
-      if (it != algo_cache().end()) {
-        chosen = it->second;
-        algo = &chosen;
-      }
-    }
-    if (algo == nullptr) {
-      if (hipblasLtMatmulAlgoGetHeuristic(h, desc, la, lb, ld, ld, pref, MAX_ALGOS, res, &found) !=
-              HIPBLAS_STATUS_SUCCESS ||
-          found < 1)
-        goto done;
-      chosen = res[tune(h, desc, la, lb, ld, g, res, found, ws, wsb, st)].algo;
-      algo = &chosen;
-      std::lock_guard<std::mutex> lock(algo_mutex());
-      algo_cache()[k2] = chosen;
-    }
-    if (hipblasLtMatmul(h, desc, &alpha, g.A, la, g.B, lb, &beta, g.D, ld, g.D, ld, algo, ws, wsb, st) ==
-        HIPBLAS_STATUS_SUCCESS)
-      err = hipSuccess;
-  }
-done:
-  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-  if (ld) hipblasLtMatrixLayoutDestroy(ld);
-  if (lb) hipblasLtMatrixLayoutDestroy(lb);
-  if (la) hipblasLtMatrixLayoutDestroy(la);
-  if (desc) hipblasLtMatmulDescDestroy(desc);
-  return err;
-}
-
-// Split of the vocabulary contraction of dh = dz W^T (output only d x N, contraction V): enough
-// slices for ~512 output tiles of 128 x 128, each slice at least 1024 entries long.
-int dh_splits(const OaceArgs& a) {
-  const int64_t tiles = ((a.d + 127) / 128) * ((a.N + 127) / 128);
-  const int64_t s = std::min<int64_t>(std::max<int64_t>(1, (512 + tiles - 1) / tiles), std::max<int64_t>(1, a.V / 1024));
-  return (int)std::min<int64_t>(s, 32);
-}
-
 }  // namespace
 
 bool oace_mfma_supported(int dtype, const OaceArgs& a) {
   if (dtype != AFA_BF16 && dtype != AFA_F16) return false;
   if (a.d % KS != 0 || a.ldh % 8 != 0 || !al16(a.h)) return false;
   if (a.w_layout == OACE_W_VD && (a.ldw % 8 != 0 || !al16(a.w))) return false;
-  if (a.N > (1 << 28) || a.V > (1 << 28)) return false;
+  if (a.N > (1 << 28) || a.V >= (1 << 24)) return false;
+  // 32-bit per-lane offsets of the backward GEMMs' direct loads
+  if (a.ldh >= (1 << 26) || (a.w_layout == OACE_W_VD && a.ldw >= (1 << 26))) return false;
   return true;
 }
 
@@ -765,7 +588,6 @@ hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, 
   if (e != hipSuccess) return e;
   char* sbase = base + l.wt + l.zc;  // the region after the cached logits
   unsigned short* dz = (unsigned short*)sbase;
-  void* bws = sbase + l.dz;
   GemmArgs g = gemm_args(a, wt, ldwt);
   g.rows = (const float*)rows;
   g.dz = dz;
@@ -787,42 +609,14 @@ hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, 
     e = launch_gemm_dt<MODE_DZ>(dtype, g, st);
   }
   if (e != hipSuccess) return e;
-  // dh (N, d) row-major = dz (N, V) W^T: column-major dh^T (d x N) = Wt^T-view (d x V) . dz^T-view (V x N).
-  // The contraction is the whole vocabulary and the output small, so it is split into S slices of
-  // the vocabulary (a strided batch into fp32 partials, plus the remainder) and reduced in order.
-  const int S = dh_splits(a);
-  if (S == 1) {
-    if ((e = blas_gemm(dtype, {false, false, a.d, a.N, a.V, wt, ldwt, 0, dz, g.ldz, 0, a.dh, a.d, 0, false, 1}, bws,
-                       l.blas, st)) != hipSuccess)
-      return e;
-  } else {
-    float* dhp = (float*)(sbase + l.dz);
-    bws = sbase + l.dz + l.dhp;
-    const int64_t vs = a.V / S, rem = a.V - vs * S, dn = a.d * a.N;
-    if ((e = blas_gemm(dtype, {false, false, a.d, a.N, vs, wt, ldwt, vs * ldwt, dz, g.ldz, vs, dhp, a.d, dn, true, S},
-                       bws, l.blas, st)) != hipSuccess)
-      return e;
-    if (rem > 0 && (e = blas_gemm(dtype, {false, false, a.d, a.N, rem, wt + S * vs * ldwt, ldwt, 0, dz + S * vs, g.ldz, 0,
-                                          dhp + S * dn, a.d, 0, true, 1}, bws, l.blas, st)) != hipSuccess)
-      return e;
-    const int parts = S + (rem > 0 ? 1 : 0);
-    const unsigned grid = (unsigned)std::min<int64_t>((dn + 255) / 256, 4096);
-    if (dtype == AFA_BF16)
-      hipLaunchKernelGGL(oace_mfma_splitk_sum_kernel<AFA_BF16>, dim3(grid), dim3(256), 0, st, (const float*)dhp, parts,
-                         dn, (unsigned short*)a.dh);
-    else
-      hipLaunchKernelGGL(oace_mfma_splitk_sum_kernel<AFA_F16>, dim3(grid), dim3(256), 0, st, (const float*)dhp, parts,
-                         dn, (unsigned short*)a.dh);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  if (a.w_layout == OACE_W_DV) {
-    // dW (d, V) row-major: column-major dW^T (V x d) = dz^T-view (V x N) . op_T(h-view (d x N))
-    return blas_gemm(dtype, {false, true, a.V, a.d, a.N, dz, g.ldz, 0, a.h, a.ldh, 0, a.dw, a.ldw, 0, false, 1}, bws,
-                     l.blas, st);
-  }
-  // dWt (V, d) row-major: column-major (d x V) = h-view (d x N) . op_T(dz-view (V x N))
-  return blas_gemm(dtype, {false, true, a.d, a.V, a.N, a.h, a.ldh, 0, dz, g.ldz, 0, a.dw, a.ldw, 0, false, 1}, bws,
-                   l.blas, st);
+  const OaceGemm gh = dh_gemm(a, wt, ldwt, dz);
+  if ((e = oace_gemm(dtype, gh, oace_gemm_parts(gh, DH_WGS), (float*)(sbase + l.dz), st)) != hipSuccess) return e;
+  const OaceGemm gw = a.w_layout == OACE_W_DV
+                          // dW (d, V): D[k][v] = sum_n dz[n][v] h[n][k]
+                          ? OaceGemm{dz, g.ldz, true, a.V, a.h, a.ldh, true, a.d, a.N, a.dw, a.ldw}
+                          // dW^T (V, d): D[v][k] = sum_n h[n][k] dz[n][v]
+                          : OaceGemm{a.h, a.ldh, true, a.d, dz, g.ldz, true, a.V, a.N, a.dw, a.ldw};
+  return oace_gemm(dtype, gw, 1, nullptr, st);
 }
 
 }  // namespace afa

@@ -131,9 +131,9 @@ def test_linear_generic_vs_oracle(shape, dtype, tied):
 @pytest.mark.parametrize("tied", [False, True])
 def test_linear_mfma_vs_oracle_and_generic(shape, dtype, tied):
     """The MFMA path (one GEMM sweep keeping the fp32 logits, the octic sums and dz from them,
-    hipBLASLt for dh and dW) against the float64 oracle on the same exact inputs and against the
-    generic kernels (AFA_FLAG_GENERIC); (512, 768, 50257) is the reference benchmark's
-    configuration (scripts/benchmark_kernels.py:118)."""
+    the MFMA GEMMs of oace_bwd_gemm.hip for dh and dW) against the float64 oracle on the same
+    exact inputs and against the generic kernels (AFA_FLAG_GENERIC); (512, 768, 50257) is the
+    reference benchmark's configuration (scripts/benchmark_kernels.py:118)."""
     N, d, V = shape
     h, w, t = _case(N, d, V, dtype, seed=N + d + V, scale=1.0 if dtype == torch.bfloat16 else 0.5)
     if tied:
