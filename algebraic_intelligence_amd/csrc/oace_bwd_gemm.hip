@@ -35,6 +35,9 @@ constexpr int GM = 256;  // A rows (m) per tile
 constexpr int GK = 32;   // contraction per step
 constexpr int OUT_PART = 0, OUT_ELEM = 1;
 constexpr int SPITCH = GM * 2 + 16;  // staged output row pitch in bytes (16-byte aligned rows)
+#ifndef OACE_GEMM_NST2
+#define OACE_GEMM_NST2 4
+#endif
 #ifndef OACE_GEMM_LONG_K
 #define OACE_GEMM_LONG_K 2048
 #endif
@@ -47,7 +50,7 @@ struct Cfg {
   static constexpr int NT = 256 * WN;  // threads
   static constexpr int NW = 4 * WN;    // waves: 4 along m (64 rows each) x WN along n (128 each)
   static constexpr int TN = 128 * WN;  // B rows (n) per tile
-  static constexpr int NST = WN == 1 ? 3 : 4;
+  static constexpr int NST = WN == 1 ? 3 : OACE_GEMM_NST2;
   static constexpr int A_BYTES = GM * GK * 2;
   static constexpr int B_BYTES = TN * GK * 2;
   static constexpr int STAGE = A_BYTES + B_BYTES;
@@ -57,7 +60,7 @@ struct Cfg {
   static constexpr int LDS = NST * STAGE;
   static constexpr int CUS_SLOTS = WN == 1 ? 2 : 1;  // workgroups per CU
   static_assert(128 * SPITCH <= LDS, "128 staged output rows must fit the ring");
-  static_assert(NST - 2 <= 2, "wait_steps covers at most two later steps");
+  static_assert(NST - 2 <= 3, "wait_steps covers at most three later steps");
 };
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -171,10 +174,11 @@ __device__ __forceinline__ u32x4_t bg_masked(const unsigned short* p, int64_t ld
 
 }  // namespace
 
-// Waits until the direct loads of at most `later` steps (0..2) issued after the one needed remain.
+// Waits until the direct loads of at most `later` steps (0..3) issued after the one needed remain.
 template <int LOADS>
 __device__ __forceinline__ void wait_steps(int later) {
-  if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * LOADS));
+  if (later >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_only(3 * LOADS));
+  else if (later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * LOADS));
   else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
   else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
 }
@@ -357,24 +361,33 @@ void oace_bwd_gemm_kernel(const BgArgs a) {
       // second element from the 8 columns it computes past them.  Sub-dword stores are slow
       // (several times the cost of the whole row segment): only an element whose dword starts in
       // the previous row or ends in the next one (at most one at each end of a row) is stored
-      // alone.  16-byte stores from the first 16-byte aligned element, dwords before and after.
+      // alone.  16-byte stores from the first 16-byte aligned element, then, in a second pass,
+      // the at most 3 + 3 dwords before and after them: the cost of a store instruction hardly
+      // depends on how many lanes it has, so those go 32 rows to an instruction.
+      struct RowSeg {
+        unsigned short* rowp;  // element m at rowp + m
+        int s0, e1, hb, nbody;
+      };
+      auto seg = [&](int n) {
+        RowSeg q;
+        q.rowp = a.out + (int64_t)n * a.ldo;
+        auto half = [&](int m) { return (int)(((uint32_t)(uintptr_t)(q.rowp + m) >> 1) & 1u); };
+        const int own_end = min(m0 + a.own, a.am);
+        q.s0 = m0 + half(m0);
+        q.e1 = own_end == a.am ? a.am - half(a.am) : own_end + half(own_end);
+        q.hb = q.s0 + (int)(((16u - ((uint32_t)(uintptr_t)(q.rowp + q.s0) & 15u)) & 15u) >> 1);
+        q.nbody = q.e1 > q.hb ? (q.e1 - q.hb) >> 3 : 0;
+        return q;
+      };
 #pragma unroll
       for (int i = 0; i < 128 * (GM / 8) / C::NT; ++i) {
         const int idx = tid + C::NT * i, r = idx / (GM / 8), c = idx % (GM / 8);
         const int n = n0 + 128 * h + r;
         if (n < a.bn) {
-          unsigned short* rowp = a.out + (int64_t)n * a.ldo;  // element m at rowp + m
-          auto half = [&](int m) { return (int)(((uint32_t)(uintptr_t)(rowp + m) >> 1) & 1u); };
-          const int own_end = min(m0 + a.own, a.am);
-          const bool last = own_end == a.am;
-          const int s0 = m0 + half(m0);
-          const int e1 = last ? a.am - half(a.am) : own_end + half(own_end);
-          const int hb = s0 + (int)(((16u - ((uint32_t)(uintptr_t)(rowp + s0) & 15u)) & 15u) >> 1);
-          const int nbody = e1 > hb ? (e1 - hb) >> 3 : 0;
-          const unsigned char* srow = lds + r * SPITCH;  // staged element m at srow + 2 (m - m0)
-          auto st16 = [&](int m) { return (unsigned)*(const unsigned short*)(srow + 2 * (m - m0)); };
-          if (c < nbody) {
-            const int e = hb - m0 + 8 * c;  // first staged index of this chunk
+          const RowSeg q = seg(n);
+          if (c < q.nbody) {
+            const unsigned char* srow = lds + r * SPITCH;  // staged element m at srow + 2 (m - m0)
+            const int e = q.hb - m0 + 8 * c;               // first staged index of this chunk
             u32x4_t v;
             if ((e & 7) == 0) {
               v = *(const u32x4_t*)(srow + 2 * e);
@@ -390,15 +403,29 @@ void oace_bwd_gemm_kernel(const BgArgs a) {
 #pragma unroll
               for (int u = 0; u < 4; ++u) v[u] = __builtin_amdgcn_alignbit(x[u + 1], x[u], 16);
             }
-            *(u32x4_t*)(rowp + m0 + e) = v;
+            *(u32x4_t*)(q.rowp + m0 + e) = v;
           }
-          if (c == GM / 8 - 1) {
-            const int hend = min(hb, e1);
-            for (int m = s0; m < hend; m += 2) *(unsigned*)(rowp + m) = st16(m) | (st16(m + 1) << 16);
-            for (int m = max(hb + 8 * nbody, hend); m < e1; m += 2)
-              *(unsigned*)(rowp + m) = st16(m) | (st16(m + 1) << 16);
-            if (m0 == 0 && half(0)) rowp[0] = (unsigned short)st16(0);
-            if (last && half(a.am) && a.am - 1 >= s0) rowp[a.am - 1] = (unsigned short)st16(a.am - 1);
+        }
+      }
+      // slots 0..5: the dwords before and after the chunks; 6 and 7: the elements stored alone
+#pragma unroll
+      for (int i = 0; i < 128 * 8 / C::NT; ++i) {
+        const int idx = tid + C::NT * i, r = idx >> 3, c = idx & 7;
+        const int n = n0 + 128 * h + r;
+        if (n < a.bn) {
+          const RowSeg q = seg(n);
+          const unsigned char* srow = lds + r * SPITCH;
+          auto st16 = [&](int m) { return (unsigned)*(const unsigned short*)(srow + 2 * (m - m0)); };
+          const int hend = min(q.hb, q.e1), tstart = max(q.hb + 8 * q.nbody, hend);
+          const int nhead = (hend - q.s0) >> 1, ndw = nhead + max(0, (q.e1 - tstart) >> 1);
+          if (c < ndw) {
+            const int m = c < nhead ? q.s0 + 2 * c : tstart + 2 * (c - nhead);
+            *(unsigned*)(q.rowp + m) = st16(m) | (st16(m + 1) << 16);
+          } else if (c == 6) {
+            if (m0 == 0 && q.s0 == 1) q.rowp[0] = (unsigned short)st16(0);
+          } else if (c == 7) {
+            if (min(m0 + a.own, a.am) == a.am && q.e1 == a.am - 1 && a.am - 1 >= q.s0)
+              q.rowp[a.am - 1] = (unsigned short)st16(a.am - 1);
           }
         }
       }

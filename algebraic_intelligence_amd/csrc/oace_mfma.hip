@@ -351,17 +351,21 @@ __global__ __launch_bounds__(256) void oace_mfma_octic_cached_kernel(const float
   }
 }
 
-// dz from the cached logits, 4 vocabulary entries per thread: the MODE_DZ epilogue's arithmetic
-// on the same fp32 logits; entries in [V, ldz) are written as zeros.
+// dz from the cached logits: the MODE_DZ epilogue's arithmetic on the same fp32 logits; entries
+// in [V, ldz) are written as zeros.  One wave per 1024 consecutive entries of a row, each lane
+// with four groups of 4 entries (all four loads in flight before the arithmetic; every load
+// and store instruction covers a contiguous 1 KB / 512 B of the row).
+constexpr int DZ_SPAN = 1024;
 template <int DT>
 __global__ __launch_bounds__(256) void oace_mfma_dz_cached_kernel(const float* zc, int64_t ldz, int N, int V,
                                                                   const float* rows, const int64_t* targets, float c0,
                                                                   const float* g_loss, unsigned short* dz) {
-  const int64_t q4 = ldz / 4;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)N * q4) return;
-  const int n = (int)(i / q4);
-  const int vs = (int)(i % q4) * 4;
+  const int lane = threadIdx.x & 63;
+  const int spans = (int)((ldz + DZ_SPAN - 1) / DZ_SPAN);
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)N * spans) return;
+  const int n = (int)(w / spans);
+  const int v0 = (int)(w % spans) * DZ_SPAN + 4 * lane;
   const float gl = g_loss ? *g_loss : 1.f;
   const float* rec = rows + (int64_t)n * OACE_ROW;
   const float tau = rec[OACE_TAU], inv_S = rec[OACE_INV_S], pc = rec[OACE_PC_INV8], radial = rec[OACE_RADIAL];
@@ -369,21 +373,33 @@ __global__ __launch_bounds__(256) void oace_mfma_dz_cached_kernel(const float* z
   const float diff = rec[OACE_SUM_P78] - pc;
   const float tc = tau * (c0 * gl);
   const int64_t t = targets[n];
-  float dzv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (vs < V) {
-    const f32x4_t z4 = *(const f32x4_t*)(zc + (int64_t)n * ldz + vs);
+  const float* zrow = zc + (int64_t)n * ldz;
+  unsigned short* drow = dz + (int64_t)n * ldz;
+  f32x4_t z4[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float x = z4[u] * tau;
-      const Oct<float> o = octic_fast(x);
-      const float bracket = scale * o.rho7 - (vs + u == t ? pc : 0.f) - (o.k8 * inv_S) * diff;
-      dzv[u] = vs + u < V ? tc * (o.r * bracket - radial * x) : 0.f;
-    }
+  for (int u = 0; u < 4; ++u) {
+    const int vs = v0 + 256 * u;
+    if (vs < V) z4[u] = *(const f32x4_t*)(zrow + vs);
   }
-  u32x2_t w;
-  w[0] = Elem<DT>::pack(dzv[0], dzv[1]);
-  w[1] = Elem<DT>::pack(dzv[2], dzv[3]);
-  *(u32x2_t*)(dz + (int64_t)n * ldz + vs) = w;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int vs = v0 + 256 * u;
+    if (vs >= ldz) continue;
+    float dzv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (vs < V) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = z4[u][e] * tau;
+        const Oct<float> o = octic_fast(x);
+        const float bracket = scale * o.rho7 - (vs + e == t ? pc : 0.f) - (o.k8 * inv_S) * diff;
+        dzv[e] = vs + e < V ? tc * (o.r * bracket - radial * x) : 0.f;
+      }
+    }
+    u32x2_t wv;
+    wv[0] = Elem<DT>::pack(dzv[0], dzv[1]);
+    wv[1] = Elem<DT>::pack(dzv[2], dzv[3]);
+    *(u32x2_t*)(drow + vs) = wv;
+  }
 }
 
 // Row records from the MODE_OCTIC partials, one wave per row.  The target logit is the dot
@@ -597,7 +613,7 @@ hipError_t oace_linear_bwd_mfma(int dtype, const OaceArgs& a, const void* rows, 
   if (l.zc > 0 && (a.flags & OACE_FLAG_Z_READY)) {
     // the forward's logits are in the workspace: dz elementwise
     const float* zcp = (const float*)(base + l.wt);
-    const unsigned dg = (unsigned)(((int64_t)a.N * (g.ldz / 4) + 255) / 256);
+    const unsigned dg = (unsigned)(((int64_t)a.N * ((g.ldz + DZ_SPAN - 1) / DZ_SPAN) + 3) / 4);
     if (dtype == AFA_BF16)
       hipLaunchKernelGGL(oace_mfma_dz_cached_kernel<AFA_BF16>, dim3(dg), dim3(256), 0, st, zcp, g.ldz, g.N, g.V,
                          (const float*)rows, a.targets, g.c0, g.g_loss, dz);
