@@ -196,19 +196,20 @@ void oace_bwd_gemm_kernel(const BgArgs a) {
   const int l32 = lane & 31, g = lane >> 5;
 
   // Workgroups that share an operand slice run consecutively on one XCD (block b runs on XCD
-  // b mod 8).  With parts: the tiles of one contraction part (both operands' slices), parts
-  // dealt to the XCDs in turn.  Without: the n tiles of one m tile (its A slice), each XCD
-  // taking a contiguous run of m tiles, so that neighbouring tiles -- which share the 128-byte
-  // lines at the ends of their output row segments when rows are not 128-byte aligned -- write
-  // them through the same L2.
+  // b mod 8), each XCD taking an equal contiguous run of work items.  With parts: items in
+  // (part, n tile, m tile) order, so that the tiles of one contraction part share both
+  // operands' slices.  Without: the n tiles of one m tile (its A slice), m tiles in order, so
+  // that neighbouring tiles -- which share the 128-byte lines at the ends of their output row
+  // segments when rows are not 128-byte aligned -- write them through the same L2.
   const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
   int part, mi, ni;
   if (a.parts > 1) {
-    const int per = a.mt * a.nt, inner = j % per;
-    part = (j / per) * 8 + xcd;
-    if (part >= a.parts) return;
-    mi = inner % a.mt;
-    ni = inner / a.mt;
+    const int tiles = a.mt * a.nt, ipx = (a.parts * tiles + 7) / 8;  // items per XCD
+    const int item = xcd * ipx + j;
+    if (j >= ipx || item >= a.parts * tiles) return;
+    part = item / tiles;
+    mi = (item % tiles) % a.mt;
+    ni = (item % tiles) / a.mt;
   } else {
     const int mpx = (a.mt + 7) / 8;  // m tiles per XCD
     part = 0;
@@ -486,7 +487,7 @@ int64_t kpart_of(int64_t K, int parts) {
 
 template <int DT, bool A_MC, bool B_MC, int OUT, int WN>
 hipError_t bg_launch(const BgArgs& g, hipStream_t st) {
-  const unsigned grid = (unsigned)(g.parts > 1 ? 8 * g.mt * g.nt * ((g.parts + 7) / 8) : 8 * g.nt * ((g.mt + 7) / 8));
+  const unsigned grid = (unsigned)(g.parts > 1 ? 8 * ((g.parts * g.mt * g.nt + 7) / 8) : 8 * g.nt * ((g.mt + 7) / 8));
   hipLaunchKernelGGL((oace_bwd_gemm_kernel<DT, A_MC, B_MC, OUT, WN>), dim3(grid), dim3(256 * WN), 0, st, g);
   return hipGetLastError();
 }
@@ -521,15 +522,28 @@ bool oace_gemm_fits(const OaceGemm& g) {
 }
 
 int oace_gemm_parts(const OaceGemm& g, int cus) {
-  // the contraction is split until every CU holds its workgroups (whole XCD groups of parts:
-  // part p runs on XCD p mod 8), in parts of at least 1024
+  // The contraction is split into the part count that minimises a model of the time: the
+  // rounds of workgroups over the CU slots, each as long as one tile over its share of the
+  // contraction, plus writing and reading the parts' fp32 partials.  Rates: a workgroup of
+  // 256 x 256 tiles (one per CU) at 6 TFLOP/s, 256 x 128 tiles (two per CU) at 3 TFLOP/s each;
+  // partials at 5 TB/s.  Parts hold at least 1024 of the contraction.
   const int wn = wn_of(g);
   const int64_t tiles = (int64_t)tiles_m(g.m) * tiles_n(g.n, wn);
-  int64_t want = cus * (wn == 1 ? Cfg<1>::CUS_SLOTS : Cfg<2>::CUS_SLOTS) / tiles;
-  if (want >= 8) want = want / 8 * 8;
-  const int64_t cap = std::max<int64_t>(1, g.k / 1024);
-  const int p = (int)std::min<int64_t>({want, cap, 64});
-  return p <= 1 ? 1 : (int)((g.k + kpart_of(g.k, p) - 1) / kpart_of(g.k, p));
+  const int64_t slots = (int64_t)cus * (wn == 1 ? Cfg<1>::CUS_SLOTS : Cfg<2>::CUS_SLOTS);
+  const double t_tile = 2.0 * GM * 128.0 * wn * (double)g.k / (wn == 1 ? 3e12 : 6e12);
+  const double t_part = 2.0 * (double)g.m * (double)g.n * 4.0 / 5e12;
+  const int pmax = (int)std::min<int64_t>(64, std::max<int64_t>(1, g.k / 1024));
+  int best = 1;
+  double best_t = 0.0;
+  for (int p = 1; p <= pmax; ++p) {
+    const double rounds = (double)((tiles * p + slots - 1) / slots);
+    const double t = rounds * t_tile / p + (p > 1 ? p * t_part : 0.0);
+    if (p == 1 || t < best_t) {
+      best = p;
+      best_t = t;
+    }
+  }
+  return best <= 1 ? 1 : (int)((g.k + kpart_of(g.k, best) - 1) / kpart_of(g.k, best));
 }
 
 size_t oace_gemm_part_bytes(const OaceGemm& g, int parts) {
