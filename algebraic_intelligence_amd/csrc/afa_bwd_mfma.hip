@@ -504,43 +504,36 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
           P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vk, P);
         }
-        float w[16], ds[16];
-        auto wscore = [&](auto exact_tag) {
-          constexpr bool E = decltype(exact_tag)::value;
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            const int lr = sub * 32 + r4 * 8 + 4 * g;     // tile row of element 4 r4
-            const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
-            const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int r = 4 * r4 + u;
-              const float s = S[r] * SQ;
-              float rr;
-              w[r] = rho8r<E>(s, rr) * i4[u];
-              ds[r] = C8 * rr * w[r] * (P[r] - e4[u]);
-            }
-          }
-        };
-        wscore(std::integral_constant<bool, !FAST>{});
+        // W and dS, masked and packed to the element type four rows at a time (only those four
+        // fp32 pairs are live next to the accumulators)
         const bool need_mask = (a.causal && m * 32 < k0_w + 31) || k0_w + 31 >= vlen || m * 32 + 31 >= L;
-        if (need_mask) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int i = m * 32 + (r >> 2) * 8 + 4 * g + (r & 3);
-            const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
-            w[r] = keep ? w[r] : 0.f;
-            ds[r] = keep ? ds[r] : 0.f;
-          }
-        }
         u32x4_t wp[2], dsp[2];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int lr = sub * 32 + r4 * 8 + 4 * g;  // tile row of element 4 r4
+          const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
+          const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
+          float w[4], ds[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            wp[kk][e] = Elem<DT>::pack(w[kk * 8 + 2 * e], w[kk * 8 + 2 * e + 1]);
-            dsp[kk][e] = Elem<DT>::pack(ds[kk * 8 + 2 * e], ds[kk * 8 + 2 * e + 1]);
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * r4 + u;
+            const float s = S[r] * SQ;
+            float rr;
+            w[u] = rho8r<!FAST>(s, rr) * i4[u];
+            ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+            if (need_mask) {
+              const int i = m * 32 + r4 * 8 + 4 * g + u;
+              const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
+              w[u] = keep ? w[u] : 0.f;
+              ds[u] = keep ? ds[u] : 0.f;
+            }
           }
+          // element r = 4 r4 + u sits in wp[r >> 3][(r & 7) >> 1]
+          wp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(w[0], w[1]);
+          wp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(w[2], w[3]);
+          dsp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(ds[0], ds[1]);
+          dsp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(ds[2], ds[3]);
+        }
 #pragma unroll
         for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
