@@ -233,3 +233,46 @@ def test_backward_after_weights_change_in_place():
     rows = {k: to_f64(cache[3][:, i:i + 1]) for i, k in enumerate(O.ROW_FIELDS)}
     rh, rw = O.fused_linear_oace_backward(hf, wf, tn, rows, g=1.0)
     assert normwise(to_f64(dh), rh) <= 2e-2 and normwise(to_f64(dw), rw) <= 2e-2
+
+
+# ------------------------------------------------------------------------------ dW row strides
+@pytest.mark.parametrize("tied,V,pad,off", [(False, 1000, 3, 0), (False, 517, 0, 0), (False, 517, 1, 1),
+                                            (False, 50257, 0, 1), (False, 2049, 8, 1), (True, 700, 1, 1),
+                                            (True, 700, 0, 0)])
+def test_dw_rows_of_any_stride_and_start(tied, V, pad, off):
+    """dW stored into rows of any stride (the weight's, odd ones included) starting at any 2-byte
+    boundary: equal to the result in a buffer of the Python layer's own, and no element outside
+    each row's dW columns changes.  Rows that are not dword aligned take the overlapping-tile stores whose seam dwords
+    are written whole; this is where an element of a neighbouring tile, of the next row or of
+    the padding would be overwritten if they were wrong."""
+    N, d = 70, 64
+    h, w, t = _case(N, d, V, torch.bfloat16, seed=V + 7 * pad + off)
+    # the weight with the padded row stride; dW gets that stride too (include/afa.h).  The
+    # reference is the Python layer's backward on the same weight (the same kernels: an odd
+    # stride of a tied embedding is not matrix-core eligible), into a buffer of its own.
+    rows_n, cols = (V, d) if tied else (d, V)
+    wide = torch.zeros((rows_n, cols + pad), dtype=torch.bfloat16, device=DEV)
+    wide[:, :cols] = w.t() if tied else w
+    wv = wide[:, :cols].t() if tied else wide[:, :cols]
+    _, cache = _fwd(h, wv, t)
+    dh_ref, dw_ref = _grads(cache)
+    hf, wop, tt, rows, gamma, _c, _s, flags, ws, _wv, _hv = cache
+    ldw = cols + pad
+    sentinel = 0x7F7B  # a bf16 NaN pattern no gradient takes
+    store = torch.full((rows_n * ldw + off + 64,), sentinel, dtype=torch.int16, device=DEV)
+    g = torch.ones((), dtype=rows.dtype, device=DEV)
+    dh = torch.empty((N, d), dtype=torch.bfloat16, device=DEV)
+    lay = A.oace.OACE_W_VD if tied else A.oace.OACE_W_DV
+    rc = _lib.lib().oace_linear_bwd(_lib.dtype_code(torch.bfloat16), N, d, V, hf.data_ptr(), hf.stride(0),
+                                    wop.data_ptr(), lay, ldw, tt.data_ptr(), float(gamma), rows.data_ptr(),
+                                    g.data_ptr(), dh.data_ptr(), store.data_ptr() + 2 * off, flags, ws.data_ptr(),
+                                    ws.numel(), _lib.stream_ptr(torch.device(DEV)))
+    _lib.check(rc, "oace_linear_bwd")
+    torch.cuda.synchronize()
+    mat = store[off:off + rows_n * ldw].view(rows_n, ldw)
+    got = mat[:, :cols].view(torch.bfloat16)
+    ref = dw_ref.t() if tied else dw_ref
+    assert normwise(to_f64(got), to_f64(ref)) <= 1e-6
+    assert normwise(to_f64(dh), to_f64(dh_ref)) <= 1e-6
+    assert bool((mat[:, cols:] == sentinel).all()), "padding columns changed"
+    assert bool((store[:off] == sentinel).all()) and bool((store[off + rows_n * ldw:] == sentinel).all())
