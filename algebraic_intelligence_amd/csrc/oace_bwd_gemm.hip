@@ -35,12 +35,7 @@ constexpr int GM = 256;  // A rows (m) per tile
 constexpr int GK = 32;   // contraction per step
 constexpr int OUT_PART = 0, OUT_ELEM = 1;
 constexpr int SPITCH = GM * 2 + 16;  // staged output row pitch in bytes (16-byte aligned rows)
-#ifndef OACE_GEMM_NST2
-#define OACE_GEMM_NST2 4
-#endif
-#ifndef OACE_GEMM_LONG_K
-#define OACE_GEMM_LONG_K 2048
-#endif
+constexpr int LONG_K = 2048;  // contractions longer than this take the 256 x 256 tiles
 
 // Tile configurations.  WN = 1: 256 x 128 tiles, 4 waves, a 3-stage ring of 24 KB stages (two
 // workgroups per CU).  WN = 2: 256 x 256 tiles, 8 waves, a 4-stage ring of 32 KB stages (one
@@ -50,7 +45,7 @@ struct Cfg {
   static constexpr int NT = 256 * WN;  // threads
   static constexpr int NW = 4 * WN;    // waves: 4 along m (64 rows each) x WN along n (128 each)
   static constexpr int TN = 128 * WN;  // B rows (n) per tile
-  static constexpr int NST = WN == 1 ? 3 : OACE_GEMM_NST2;
+  static constexpr int NST = WN == 1 ? 3 : 4;  // a 5th stage for WN = 2 measured no faster
   static constexpr int A_BYTES = GM * GK * 2;
   static constexpr int B_BYTES = TN * GK * 2;
   static constexpr int STAGE = A_BYTES + B_BYTES;
@@ -60,7 +55,7 @@ struct Cfg {
   static constexpr int LDS = NST * STAGE;
   static constexpr int CUS_SLOTS = WN == 1 ? 2 : 1;  // workgroups per CU
   static_assert(128 * SPITCH <= LDS, "128 staged output rows must fit the ring");
-  static_assert(NST - 2 <= 3, "wait_steps covers at most three later steps");
+  static_assert(NST - 2 <= 2, "wait_steps is given at most two later steps");
 };
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -174,11 +169,10 @@ __device__ __forceinline__ u32x4_t bg_masked(const unsigned short* p, int64_t ld
 
 }  // namespace
 
-// Waits until the direct loads of at most `later` steps (0..3) issued after the one needed remain.
+// Waits until the direct loads of at most `later` steps (0..2) issued after the one needed remain.
 template <int LOADS>
 __device__ __forceinline__ void wait_steps(int later) {
-  if (later >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_only(3 * LOADS));
-  else if (later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * LOADS));
+  if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * LOADS));
   else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
   else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
 }
@@ -474,7 +468,7 @@ namespace {
 // Tile configuration of a GEMM: 256 x 256 tiles for a long contraction (split into parts when
 // the tiles are few: fewer partials), 256 x 128 tiles with two workgroups per CU for a short
 // one (their loops overlap each other's prologue and epilogue).
-int wn_of(const OaceGemm& g) { return g.k > OACE_GEMM_LONG_K ? 2 : 1; }
+int wn_of(const OaceGemm& g) { return g.k > LONG_K ? 2 : 1; }
 
 int tiles_m(int64_t m, int own = GM) { return (int)((m + own - 1) / own); }
 int tiles_n(int64_t n, int wn) { return (int)((n + 128 * wn - 1) / (128 * wn)); }
