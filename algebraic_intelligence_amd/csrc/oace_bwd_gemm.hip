@@ -9,7 +9,7 @@
 // workgroups per CU, for a short contraction; WN = 2, eight waves and one workgroup per CU, for a
 // long one).  Each operand is read from memory in one of two orientations:
 //   K-contiguous (KC): element (r, k) at p[r * ld + k]; the LDS tile holds 64-byte rows (32 k of
-//     one r), 16-byte chunks swizzled by (r >> 1) & 3, and a fragment is one 16-byte read;
+//     one r), 16-byte chunks swizzled by (r >> 2) & 3, and a fragment is one 16-byte read;
 //   row-contiguous (MC): element (r, k) at p[k * ld + r]; the LDS tile holds the 32 k rows of the
 //     tile's r range, 16-byte chunks swizzled by (k & 3) << 2 (conflict-free), and a fragment is
 //     two ds_read_tr16_b64, which return 4 k rows of one r column per lane.
@@ -91,7 +91,7 @@ __device__ __forceinline__ f32x16_t bg_mma(u32x4_t a, u32x4_t b, f32x16_t c) {
 template <bool MC, int R>
 __device__ __forceinline__ int bg_off(int row, int c) {
   if constexpr (MC) return row * (R * 2) + ((c ^ ((row & 3) << 2)) << 4);
-  else return row * 64 + ((c ^ ((row >> 1) & 3)) << 4);
+  else return row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
 }
 
 // (tile row, logical chunk) of the 16-byte slot s (physical position s * 16 of the stage).
@@ -103,7 +103,7 @@ __device__ __forceinline__ void bg_slot(int s, int& row, int& c) {
     c = (s % CPR) ^ ((row & 3) << 2);
   } else {
     row = s >> 2;
-    c = (s & 3) ^ ((row >> 1) & 3);
+    c = (s & 3) ^ ((row >> 2) & 3);
   }
 }
 

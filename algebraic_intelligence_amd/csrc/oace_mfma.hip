@@ -16,8 +16,8 @@
 // 64 x 128, each a 2 x 4 grid of 32x32x16 MFMA blocks whose accumulator lanes hold one row and 16
 // vocabulary entries, so the row reductions are in-lane.  K (d_model) advances 32 per step
 // through a 3-stage LDS ring filled by direct global -> LDS loads (64-byte rows, 16-byte chunks
-// swizzled by (row >> 1) & 3: conflict-free 32-row fragment reads), one barrier per step.  Tiles
-// of one vocabulary block are dispatched consecutively on one XCD (they share its W tile in L2).
+// swizzled by (row >> 2) & 3: 16 consecutive rows in 16 distinct bank groups), one barrier per
+// step.  Tiles of one vocabulary block are dispatched consecutively on one XCD (they share its W tile in L2).
 // W is used as W^T (vocab, d_model) with d_model contiguous: a tied embedding already is; the
 // (d_model, vocab) output head is transposed once per call into the workspace.
 #include <algorithm>
@@ -71,7 +71,7 @@ __device__ __forceinline__ f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
 __host__ __device__ constexpr int vm_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
 // Byte offset of logical 16-byte chunk lc of row r in a tile of 64-byte rows.
-__device__ __forceinline__ int chunk_off(int r, int lc) { return r * 64 + ((lc ^ ((r >> 1) & 3)) << 4); }
+__device__ __forceinline__ int chunk_off(int r, int lc) { return r * 64 + ((lc ^ ((r >> 2) & 3)) << 4); }
 
 }  // namespace
 
@@ -96,12 +96,12 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
   const unsigned short* bsrc[B_LOADS];
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
-    const int s = 256 * i + tid, r = s >> 2, lc = (s & 3) ^ ((r >> 1) & 3);
+    const int s = 256 * i + tid, r = s >> 2, lc = (s & 3) ^ ((r >> 2) & 3);
     asrc[i] = a.wt + (int64_t)min(v0 + r, a.V - 1) * a.ldwt + lc * 8;
   }
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
-    const int s = 256 * i + tid, r = s >> 2, lc = (s & 3) ^ ((r >> 1) & 3);
+    const int s = 256 * i + tid, r = s >> 2, lc = (s & 3) ^ ((r >> 2) & 3);
     bsrc[i] = a.h + (int64_t)min(n0 + r, a.N - 1) * a.ldh + lc * 8;
   }
   auto issue = [&](int t) {
