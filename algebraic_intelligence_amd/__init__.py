@@ -2,7 +2,8 @@
 
 A drop-in for the AFA hot path of tasmaikeni13/algebraic-intelligence: the fused forward
 (pallas_afa_forward / tiled_afa_forward), its analytical backward (pallas_afa custom VJP),
-the padding front door (algebraic_flash_attention), the A-Softmax (algebraic_softmax), the
+the padding front door (algebraic_flash_attention), the sequence ring (distributed_ring_afa, its
+hops run in turn on one GPU), the A-Softmax (algebraic_softmax), the
 octic weight (octic_kernel), the Cayley rotary (AGO) tables and rotation, and the OACE loss head
 (fused_linear_oace, fused_oace_softmax_loss) — all running in hand-written HIP kernels behind the
 C ABI of include/afa.h.
@@ -10,6 +11,7 @@ C ABI of include/afa.h.
 from .afa import (
     afa_flops,
     algebraic_flash_attention,
+    distributed_ring_afa,
     exact_afa_reference,
     exact_afa_with_denominator,
     pallas_afa,
@@ -33,7 +35,7 @@ from .oace import (
 )
 
 __all__ = [
-    "afa_flops", "algebraic_flash_attention", "exact_afa_reference", "exact_afa_with_denominator",
+    "afa_flops", "algebraic_flash_attention", "distributed_ring_afa", "exact_afa_reference", "exact_afa_with_denominator",
     "pallas_afa", "pallas_afa_forward", "tiled_afa_backward", "tiled_afa_forward",
     "CayleyRotary", "algebraic_softmax", "apply_ago_rotations", "build_cayley_rotary_matrix",
     "octic_kernel", "rotate_tensor", "fused_linear_oace", "fused_linear_oace_forward",

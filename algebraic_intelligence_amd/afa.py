@@ -25,7 +25,7 @@ from ._lib import table_2d
 
 __all__ = [
     "pallas_afa_forward", "tiled_afa_forward", "exact_afa_reference", "exact_afa_with_denominator",
-    "tiled_afa_backward", "pallas_afa", "algebraic_flash_attention",
+    "tiled_afa_backward", "pallas_afa", "algebraic_flash_attention", "distributed_ring_afa",
 ]
 
 
@@ -276,6 +276,85 @@ def algebraic_flash_attention(
     if q.shape[-1] > 128 and q.shape[-1] % 128 != 0:
         raise ValueError("head dimensions above 128 must be divisible by 128")
     return _PallasAFA.apply(q, k, v, float(sink_omega), bool(causal), None, rotary_params)
+
+
+def _device_major(t: torch.Tensor, n: int) -> torch.Tensor:
+    """(B, H, n * S, D) contiguous -> the (n, B * H, S, D) view whose batch axis is the shard."""
+    B, H, L, D = t.shape
+    S = L // n
+    return t.as_strided((n, B * H, S, D), (S * D, L * D, D, 1), t.storage_offset())
+
+
+def distributed_ring_afa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    sink_omega: float = 0.5,
+    causal: bool = False,
+    axis_name: str = "devices",
+    num_devices: int = 16,
+) -> torch.Tensor:
+    """Ring AFA over ``num_devices`` sequence shards (src/kernels/pallas_afa.py:618-662).
+
+    The reference runs once per device inside a mesh: device d holds query shard d, the key and
+    value shards travel round the ring, and hop h adds rho(s)^8-weighted sums of shard
+    (d - h) mod n to fp32 accumulators; out = o / (d + sink_omega) after n hops.  Here, on one
+    GPU, q, k and v are the whole (B, H, L, D) arrays, L = num_devices * shard_len, device d's
+    shard being rows [d * shard_len, (d + 1) * shard_len), and the result is the devices' outputs
+    side by side.  A hop is one afa_fwd call with AFA_FLAG_ACCUMULATE over every device's pair at
+    once (two where the ring wraps round): the devices are the batch axis of strided views, so no
+    shard moves.  causal: hop 0 pairs each shard with itself under the causal mask, and at hop
+    h > 0 only devices d >= h hold an earlier shard; the later ones (masked whole in the
+    reference) are not computed.  The accumulators are fp32 (fp64 for fp64 inputs); the final
+    division is afa_ring_finish.  ``axis_name`` is accepted for signature compatibility.
+    """
+    del axis_name
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must all have shape (batch, heads, sequence, dimension)")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q, k, and v shapes must match, got {tuple(q.shape)}, {tuple(k.shape)}, and {tuple(v.shape)}")
+    if not _finite_nonneg(sink_omega):
+        raise ValueError("sink_omega must be finite and nonnegative")
+    n = int(num_devices)
+    B, H, L, D = q.shape
+    if n <= 0 or L % n != 0:
+        raise ValueError(f"seq_len ({L}) must split into num_devices ({num_devices}) equal shards")
+    dev = _lib.require_device(q, k, v)
+    dt = _lib.dtype_code(q.dtype)
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError(f"q, k and v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    S = L // n
+    qd, kd, vd = (_device_major(t.contiguous(), n) for t in (q, k, v))
+    acc = torch.zeros((B, H, L, D), dtype=_lib.accum_dtype(q.dtype), device=dev)
+    den = torch.zeros((n, B * H, S), dtype=acc.dtype, device=dev)
+    out = torch.empty((B, H, L, D), dtype=q.dtype, device=dev)
+    accd = _device_major(acc, n)
+    L_ = _lib.lib()
+    with torch.cuda.device(dev):
+        stream = _lib.stream_ptr(dev)
+        ws_bytes = max(L_.afa_fwd_workspace_size(dt, m, B * H, S, D, 0) for m in range(1, n + 1))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+
+        def hop_call(d0, d1, kv0, diag):
+            # devices d0 .. d1-1 against key/value shards kv0 .. kv0 + d1 - d0 - 1
+            m = d1 - d0
+            qs, ks, vs, os_ = qd[d0:d1], kd[kv0:kv0 + m], vd[kv0:kv0 + m], accd[d0:d1]
+            rc = L_.afa_fwd(dt, m, B * H, S, D, _lib.ptr(qs), _lib.ptr(ks), _lib.ptr(vs),
+                            _strides(qs, ks, vs, os_), _lib.ptr(os_), _lib.ptr(den[d0:d1]), None,
+                            None, 0, 0.0, int(diag), 0, _lib.FLAG_ACCUMULATE, _lib.ptr(ws), ws_bytes,
+                            stream)
+            _lib.check(rc, "afa_fwd")
+
+        for hop in range(n):
+            # devices d >= hop read shard d - hop; devices d < hop read shard d - hop + n
+            hop_call(hop, n, 0, causal and hop == 0)
+            if hop > 0 and not causal:
+                hop_call(0, hop, n - hop, False)
+        st = (ctypes.c_int64 * 6)(S * D, L * D, D, S * D, L * D, D)
+        rc = L_.afa_ring_finish(dt, n, B * H, S, D, _lib.ptr(acc), _lib.ptr(den), st, float(sink_omega),
+                                _lib.ptr(out), stream)
+    _lib.check(rc, "afa_ring_finish")
+    return out
 
 
 def afa_flops(batch: int, heads: int, seq_len: int, head_dim: int, causal: bool) -> int:

@@ -383,6 +383,27 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
 
   // epilogue
   const float tot = rowsum + __shfl_xor(rowsum, 32) + a.omega;
+  if (a.acc) {
+    // a hop of a ring / one key shard: the unnormalised sums are added to the caller's fp32
+    // accumulators (every element of this block's rows belongs to this lane alone)
+    if (qi < L) {
+      float* op = (float*)a.out + b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int f = db * 32 + r4 * 8 + 4 * g;
+          if (D == DP || f < D) {
+            f32x4_t x = *(const f32x4_t*)(op + f);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] += o[db][r4 * 4 + u] * a.w_unscale;
+            *(f32x4_t*)(op + f) = x;
+          }
+        }
+      if (g == 0) a.denom[(int64_t)bh * L + qi] += (tot - a.omega) * a.w_unscale;
+    }
+    return;
+  }
   if (qi < L) {
     unsigned short* op = (unsigned short*)a.out + b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
     const float inv = 1.0f / tot;

@@ -213,7 +213,14 @@ __global__ __launch_bounds__(256) void afa_fwd_generic_kernel(const GenArgs a) {
       dsum += a.exact_ref ? pv : p;
     }
   }
-  if (qi < a.L) {
+  if (qi < a.L && a.acc) {
+    // a hop of a ring / one key shard: the unnormalised sums added to the caller's accumulators
+    const int64_t obase = b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (sub + 8 * m < D) ((T*)a.out)[obase + sub + 8 * m] += o[m];
+    if (sub == 0) ((T*)a.denom)[(int64_t)bh * a.L + qi] += dsum;
+  } else if (qi < a.L) {
     const T tot = dsum + (T)a.omega;
     const int64_t obase = b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
     if (a.exact_ref) {
@@ -498,6 +505,37 @@ hipError_t generic_bwd_launch(int dtype, const GenArgs& a, hipStream_t st) {
     case AFA_F16: return gen_bwd_dt<AFA_F16>(a, rot, st);
     default: return gen_bwd_dt<AFA_F64>(a, rot, st);
   }
+}
+
+// ------------------------------------------------------------------------------ ring finish
+// The final division of a ring's accumulators (src/kernels/pallas_afa.py:660-661):
+// out = acc / (denom + sink) in the accumulation type, rounded to the input dtype.  One thread
+// per output element; acc and out are strided (b, h, l, contiguous features), denom is
+// contiguous over (b, h, l).
+template <int DT>
+__global__ __launch_bounds__(256) void afa_ring_finish_kernel(const RingFinish r) {
+  typedef typename Acc<DT>::T T;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)r.B * r.H * r.L * r.D) return;
+  const int64_t row = i / r.D;
+  const int64_t f = i - row * r.D;
+  const int64_t l = row % r.L, bh = row / r.L;
+  const int64_t h = bh % r.H, b = bh / r.H;
+  const T d = ((const T*)r.denom)[row] + (T)r.sink;
+  const T x = ((const T*)r.acc)[b * r.a_b + h * r.a_h + l * r.a_l + f];
+  st<DT>(r.out, b * r.o_b + h * r.o_h + l * r.o_l + f, x / d);
+}
+
+hipError_t ring_finish_launch(int dtype, const RingFinish& r, hipStream_t st) {
+  const int64_t n = (int64_t)r.B * r.H * r.L * r.D;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  switch (dtype) {
+    case AFA_F32: hipLaunchKernelGGL((afa_ring_finish_kernel<AFA_F32>), grid, dim3(256), 0, st, r); break;
+    case AFA_BF16: hipLaunchKernelGGL((afa_ring_finish_kernel<AFA_BF16>), grid, dim3(256), 0, st, r); break;
+    case AFA_F16: hipLaunchKernelGGL((afa_ring_finish_kernel<AFA_F16>), grid, dim3(256), 0, st, r); break;
+    default: hipLaunchKernelGGL((afa_ring_finish_kernel<AFA_F64>), grid, dim3(256), 0, st, r); break;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace afa

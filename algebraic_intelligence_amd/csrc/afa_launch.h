@@ -43,6 +43,9 @@ struct FwdArgs {
   int ks_items;
   float* ks_part;
   int* ks_cnt;
+  // AFA_FLAG_ACCUMULATE: out is fp32 (element strides o_*) and receives += the unnormalised
+  // numerator, denom += the row sum (sink_omega is 0)
+  int acc;
 };
 
 // Key split of the pipelined kernel for one shape: causal rows near the end of a long sequence,
@@ -77,6 +80,7 @@ struct GenArgs {
   int valid_len;
   int causal;
   int exact_ref;
+  int acc;  // forward, AFA_FLAG_ACCUMULATE: out and denom (accumulation type) receive += sums
   double scale;
   double omega;
   // fast-rho guard of the MFMA backward (as FwdArgs): per 64-row block bounds of q (for the dK/dV
@@ -153,6 +157,17 @@ hipError_t asoftmax_fwd_launch(int dtype, int64_t rows, int64_t n, const void* x
 hipError_t asoftmax_bwd_launch(int dtype, int64_t rows, int64_t n, const void* x, const void* g,
                                void* dx, double sink, double eps, hipStream_t st);
 hipError_t octic_fwd_launch(int dtype, int64_t n, const void* x, void* y, hipStream_t st);
+
+// Final division of a ring's accumulators (afa_generic.hip); strides in elements.
+struct RingFinish {
+  const void* acc;    // fp32 (fp64 for AFA_F64) numerators
+  const void* denom;  // row sums, contiguous over (b, h, l)
+  void* out;          // the input dtype
+  int64_t a_b, a_h, a_l, o_b, o_h, o_l;
+  int B, H, L, D;
+  double sink;
+};
+hipError_t ring_finish_launch(int dtype, const RingFinish& r, hipStream_t st);
 hipError_t octic_bwd_launch(int dtype, int64_t n, const void* x, const void* g, void* dx,
                             hipStream_t st);
 

@@ -12,6 +12,7 @@ reference repository (tasmaikeni13/algebraic-intelligence):
                                  (oracle form: tests/reference_attention.py:5-13)
   AFA forward .................. src/kernels/pallas_afa.py:52-151 (kernel), :267-327 (exact),
                                  :330-406 (tiled); tests/reference_attention.py:44-59
+  ring AFA (per device, hop) .. src/kernels/pallas_afa.py:618-662 (distributed_ring_afa)
   AFA backward (VJP) ........... src/kernels/pallas_afa.py:409-522
   A-Softmax (+VJP) ............. src/attention.py:53-91, src/primitives.py:56-79;
                                  tests/reference_attention.py:16-36
@@ -23,6 +24,8 @@ Pinning (what checks each function; the tests live in tests/test_oracle.py):
                   50-digit mpmath evaluation; derivative 8*rho^8/sqrt(1+x^2) by finite differences
   afa_forward     50-digit mpmath brute force on tiny inputs; scale invariance; causal prefix
                   invariance; split-K (ring) additivity; L=1 closed form
+  ring_afa        equals afa_forward for every shard count, causal and not (the hops only
+                  re-associate the sums); one shard reduces to afa_forward itself
   afa_backward    central finite differences of afa_forward (float64)
   asoftmax        Jacobian at 0 = [[2,-2],[-2,2]] (sink 0); simplex bounds; VJP by finite differences;
                   mpmath brute force
@@ -35,7 +38,7 @@ from __future__ import annotations
 import numpy as np
 
 __all__ = [
-    "rho", "rho8", "rho8_derivative", "afa_forward", "afa_backward", "afa_flops",
+    "rho", "rho8", "rho8_derivative", "afa_forward", "ring_afa", "afa_backward", "afa_flops",
     "asoftmax", "asoftmax_vjp", "cayley_base", "cayley_tables", "default_freqs",
     "rotate_pairs", "ago_apply",
 ]
@@ -109,6 +112,41 @@ def afa_forward(q, k, v, sink_omega=0.5, causal=False, valid_len=None, rotary=No
     out = num / den
     if return_denominator:
         return out, den
+    return out
+
+
+def ring_afa(q, k, v, sink_omega=0.5, causal=False, num_devices=16):
+    """The ring of src/kernels/pallas_afa.py:618-662 in float64, every device in turn.
+
+    q, k, v: (..., L, D) with L = num_devices * shard_len; device d holds rows
+    [d * shard_len, (d + 1) * shard_len) of each.  At hop h device d holds key/value shard
+    kv = (d - h) mod n and adds p = rho(q_d k_kv^T / sqrt(D))^8 to its sums: o += p v_kv,
+    den += sum_j p.  causal: p is kept where the global column index <= the global row index
+    and the whole tile is dropped when kv > d (which the index rule already implies).
+    out_d = o / (den + sink_omega); the devices' outputs are returned side by side.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    n = num_devices
+    L, D = q.shape[-2], q.shape[-1]
+    S = L // n
+    out = np.empty_like(q)
+    rows = np.arange(S)[:, None]
+    cols = np.arange(S)[None, :]
+    for d in range(n):
+        qd = q[..., d * S:(d + 1) * S, :]
+        o = np.zeros_like(qd)
+        den = np.zeros(qd.shape[:-1] + (1,))
+        for hop in range(n):
+            kv = (d - hop) % n
+            kd, vd = k[..., kv * S:(kv + 1) * S, :], v[..., kv * S:(kv + 1) * S, :]
+            p = rho8(np.einsum("...id,...jd->...ij", qd, kd) / np.sqrt(D))
+            if causal:
+                p = np.where((cols + kv * S <= rows + d * S) & (kv <= d), p, 0.0)
+            o += np.einsum("...ij,...jd->...id", p, vd)
+            den += p.sum(axis=-1, keepdims=True)
+        out[..., d * S:(d + 1) * S, :] = o / (den + sink_omega)
     return out
 
 

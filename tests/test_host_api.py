@@ -49,6 +49,23 @@ def test_valid_calls_on_host_tensors_fail_loudly(fn):
         fn(q, k, v, causal=True)
 
 
+def test_ring_argument_checks():
+    """distributed_ring_afa (src/kernels/pallas_afa.py:618-662): shapes, sink and the shard count
+    are checked first; a valid call on host tensors raises (no CPU implementation)."""
+    q, k, v = _qkv()
+    with pytest.raises(ValueError):
+        A.distributed_ring_afa(q[0], k[0], v[0])
+    with pytest.raises(ValueError):
+        A.distributed_ring_afa(q, k[:, :, :64], v)
+    with pytest.raises(ValueError, match="sink_omega"):
+        A.distributed_ring_afa(q, k, v, sink_omega=-1.0)
+    for n in (0, -2, 3, 256):
+        with pytest.raises(ValueError, match="num_devices"):
+            A.distributed_ring_afa(q, k, v, num_devices=n)
+    with pytest.raises(RuntimeError, match="GPU"):
+        A.distributed_ring_afa(q, k, v, causal=True, num_devices=4)
+
+
 def test_algebraic_softmax_checks():
     x = torch.zeros(4, 8)
     for bad in (-0.1, math.nan, math.inf):

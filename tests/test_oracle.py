@@ -141,6 +141,18 @@ def test_ring_split_additivity():
     assert normwise(num / (den + sink), full) < 1e-14
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_ring_oracle_equals_full_attention(causal):
+    """The ring of src/kernels/pallas_afa.py:618-662 re-associates the sums of the full forward:
+    for every shard count it gives the same output (a causal mask on shard-local indices, or a
+    wrong shard offset, would not)."""
+    rng = np.random.default_rng(15)
+    q, k, v = rng.standard_normal((3, 2, 2, 32, 8)) * 0.6
+    full = O.afa_forward(q, k, v, 0.5, causal=causal)
+    for n in (1, 2, 4, 8):
+        assert normwise(O.ring_afa(q, k, v, 0.5, causal, n), full) < 1e-13, n
+
+
 def test_value_linearity_and_key_permutation():
     rng = np.random.default_rng(6)
     q, k, v, v2 = rng.standard_normal((4, 1, 2, 24, 8))
