@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_PKG, "_build", "libafa_hip.so")
 
 AFA_F32, AFA_BF16, AFA_F16, AFA_F64 = 0, 1, 2, 3
 FLAG_EXACT_TAIL, FLAG_GENERIC, FLAG_EXACT_REF, FLAG_SIMPLE_SCHEDULE = 0x1, 0x2, 0x4, 0x8
-FLAG_ACCUMULATE = 0x100
+FLAG_ACCUMULATE, FLAG_PARTIAL = 0x100, 0x200
 
 (OK, ERR_NULL, ERR_DTYPE, ERR_SHAPE, ERR_HEAD_DIM, ERR_SINK, ERR_VALID_LEN, ERR_EPS, ERR_ROTARY,
  ERR_ALIGN, ERR_WORKSPACE, ERR_UNSUPPORTED, ERR_GAMMA, ERR_SCRATCH_LIMIT) = range(14)

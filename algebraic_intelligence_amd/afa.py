@@ -301,12 +301,13 @@ def distributed_ring_afa(
     (d - h) mod n to fp32 accumulators; out = o / (d + sink_omega) after n hops.  Here, on one
     GPU, q, k and v are the whole (B, H, L, D) arrays, L = num_devices * shard_len, device d's
     shard being rows [d * shard_len, (d + 1) * shard_len), and the result is the devices' outputs
-    side by side.  A hop is one afa_fwd call with AFA_FLAG_ACCUMULATE over every device's pair at
-    once (two where the ring wraps round): the devices are the batch axis of strided views, so no
-    shard moves.  causal: hop 0 pairs each shard with itself under the causal mask, and at hop
-    h > 0 only devices d >= h hold an earlier shard; the later ones (masked whole in the
-    reference) are not computed.  The accumulators are fp32 (fp64 for fp64 inputs); the final
-    division is afa_ring_finish.  ``axis_name`` is accepted for signature compatibility.
+    side by side.  A hop is one afa_fwd call over every device's pair at once (two where the ring
+    wraps round): the devices are the batch axis of strided views, so no shard moves.  Hop 0
+    stores the sums (AFA_FLAG_PARTIAL, so the accumulators need no clearing), every later hop adds
+    to them (AFA_FLAG_ACCUMULATE).  causal: hop 0 pairs each shard with itself under the causal
+    mask, and at hop h > 0 only devices d >= h hold an earlier shard; the later ones (masked whole
+    in the reference) are not computed.  The accumulators are fp32 (fp64 for fp64 inputs); the
+    final division is afa_ring_finish.  ``axis_name`` is accepted for signature compatibility.
     """
     del axis_name
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
@@ -325,8 +326,8 @@ def distributed_ring_afa(
         raise TypeError(f"q, k and v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
     S = L // n
     qd, kd, vd = (_device_major(t.contiguous(), n) for t in (q, k, v))
-    acc = torch.zeros((B, H, L, D), dtype=_lib.accum_dtype(q.dtype), device=dev)
-    den = torch.zeros((n, B * H, S), dtype=acc.dtype, device=dev)
+    acc = torch.empty((B, H, L, D), dtype=_lib.accum_dtype(q.dtype), device=dev)
+    den = torch.empty((n, B * H, S), dtype=acc.dtype, device=dev)
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=dev)
     accd = _device_major(acc, n)
     L_ = _lib.lib()
@@ -335,20 +336,20 @@ def distributed_ring_afa(
         ws_bytes = max(L_.afa_fwd_workspace_size(dt, m, B * H, S, D, 0) for m in range(1, n + 1))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
 
-        def hop_call(d0, d1, kv0, diag):
+        def hop_call(d0, d1, kv0, diag, flags=_lib.FLAG_ACCUMULATE):
             # devices d0 .. d1-1 against key/value shards kv0 .. kv0 + d1 - d0 - 1
             m = d1 - d0
             qs, ks, vs, os_ = qd[d0:d1], kd[kv0:kv0 + m], vd[kv0:kv0 + m], accd[d0:d1]
             rc = L_.afa_fwd(dt, m, B * H, S, D, _lib.ptr(qs), _lib.ptr(ks), _lib.ptr(vs),
                             _strides(qs, ks, vs, os_), _lib.ptr(os_), _lib.ptr(den[d0:d1]), None,
-                            None, 0, 0.0, int(diag), 0, _lib.FLAG_ACCUMULATE, _lib.ptr(ws), ws_bytes,
-                            stream)
+                            None, 0, 0.0, int(diag), 0, flags, _lib.ptr(ws), ws_bytes, stream)
             _lib.check(rc, "afa_fwd")
 
-        for hop in range(n):
+        hop_call(0, n, 0, causal, _lib.FLAG_PARTIAL)  # every device against its own shard
+        for hop in range(1, n):
             # devices d >= hop read shard d - hop; devices d < hop read shard d - hop + n
-            hop_call(hop, n, 0, causal and hop == 0)
-            if hop > 0 and not causal:
+            hop_call(hop, n, 0, False)
+            if not causal:
                 hop_call(0, hop, n - hop, False)
         st = (ctypes.c_int64 * 6)(S * D, L * D, D, S * D, L * D, D)
         rc = L_.afa_ring_finish(dt, n, B * H, S, D, _lib.ptr(acc), _lib.ptr(den), st, float(sink_omega),

@@ -159,9 +159,9 @@ FwdPlan fwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, int64_t 
                  bool mfma_layout, bool f32_layout, bool in_head_32, unsigned flags, int causal) {
   FwdPlan p;
   if (flags & (AFA_FLAG_GENERIC | AFA_FLAG_EXACT_REF)) return p;
-  // accumulate calls take the kernels that have the accumulating epilogue: the 128-query
-  // pipelined kernel (bf16/fp16) and the generic one
-  const bool acc = (flags & AFA_FLAG_ACCUMULATE) != 0;
+  // key-shard calls (partial or accumulating) take the kernels with that epilogue: the pipelined
+  // bf16/fp16 kernels, the fp32 matrix-core kernel and the generic one
+  const bool acc = (flags & (AFA_FLAG_ACCUMULATE | AFA_FLAG_PARTIAL)) != 0;
   const bool fused_ok = !acc && afa::mfma_fwd_supported(dtype, (int)D);
   const bool pipe_ok = afa::pipe_fwd_supported(dtype, (int)D) && in_head_32;
   if ((fused_ok || pipe_ok) && mfma_layout) {
@@ -173,7 +173,7 @@ FwdPlan fwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, int64_t 
       // workgroups with several waves per SIMD (afa_fwd_pipe.hip).  With a single round (C4: 512
       // workgroups on 256 CUs) the finer causal blocks of the 128-query kernel balance better:
       // 0.0545 against 0.0560 ms, measured on one box.
-      p.wide = !acc && D == 64 && B * H * ((L + 255) / 256) >= 3 * (int64_t)cu_count();
+      p.wide = D == 64 && B * H * ((L + 255) / 256) >= 3 * (int64_t)cu_count();
       if (rotary) {
         p.rotk = true;
         p.krot = off;
@@ -204,7 +204,7 @@ FwdPlan fwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, int64_t 
     p.total = off;
     return p;
   }
-  if (!acc && dtype == AFA_F32 && afa::f32_fwd_supported((int)D) && f32_layout) {
+  if (dtype == AFA_F32 && afa::f32_fwd_supported((int)D) && f32_layout) {
     p.kind = FWD_F32;
     // fewer 128-query workgroups than CUs: split every query block's key tiles over up to
     // 2 * CUs workgroups in all (partials in the workspace, then a combine kernel)
@@ -262,8 +262,8 @@ size_t afa_fwd_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t s
                               int rotary) {
   if (fwd_check(dtype, batch, heads, seq_len, head_dim) != AFA_OK) return 0;
   const bool in_head = (seq_len - 1) * head_dim + head_dim < (int64_t(1) << 31);
-  // the larger of the default plan and the accumulating one (which never takes the 256-query
-  // kernel, so it may split keys where the default plan does not)
+  // the larger of the default plan and the key-shard one (which never takes the fully fused
+  // kernel, so it may need the pipelined kernels' workspace where the default plan does not)
   return std::max(
       fwd_plan(dtype, batch, heads, seq_len, head_dim, seq_len, rotary != 0, true, true, in_head, 0, -1).total,
       fwd_plan(dtype, batch, heads, seq_len, head_dim, seq_len, rotary != 0, true, true, in_head,
@@ -282,8 +282,10 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   if (valid_len < 0 || valid_len > seq_len) return AFA_ERR_VALID_LEN;
   rc = check_rotary(rot_cos, rot_sin, rot_len, seq_len, head_dim);
   if (rc != AFA_OK) return rc;
-  const bool acc = (flags & AFA_FLAG_ACCUMULATE) != 0;
-  if (acc && denom == nullptr) return AFA_ERR_NULL;  // the row sums' accumulator
+  const unsigned shard_flags = flags & (AFA_FLAG_ACCUMULATE | AFA_FLAG_PARTIAL);
+  if (shard_flags == (AFA_FLAG_ACCUMULATE | AFA_FLAG_PARTIAL)) return AFA_ERR_UNSUPPORTED;
+  const int acc = shard_flags == AFA_FLAG_PARTIAL ? afa::ACC_STORE : shard_flags ? afa::ACC_ADD : afa::ACC_NONE;
+  if (acc && denom == nullptr) return AFA_ERR_NULL;  // the row sums' array
   if (acc && sink_omega != 0.0) return AFA_ERR_SINK;  // the sink belongs to the final division
   const int vlen = valid_len == 0 ? (int)seq_len : (int)valid_len;
   const Strides st = resolve_strides(strides, heads, seq_len, head_dim);
@@ -327,7 +329,7 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
   a.B = (int)batch; a.H = (int)heads; a.L = (int)seq_len;
   a.valid_len = vlen;
   a.causal = causal ? 1 : 0;
-  a.acc = acc ? 1 : 0;
+  a.acc = acc;
   a.omega = (float)sink_omega;
   a.q_scale = 1.0f;
   a.w_unscale = 1.0f;
@@ -390,7 +392,7 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
     g.valid_len = vlen;
     g.causal = causal ? 1 : 0;
     g.exact_ref = (flags & AFA_FLAG_EXACT_REF) ? 1 : 0;
-    g.acc = acc ? 1 : 0;
+    g.acc = acc;
     g.scale = 1.0 / std::sqrt((double)head_dim);
     if (dtype != AFA_F64) g.scale = (double)(float)g.scale;
     g.omega = dtype == AFA_F64 ? sink_omega : (double)(float)sink_omega;

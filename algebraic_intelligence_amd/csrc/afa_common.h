@@ -83,6 +83,14 @@ struct Elem<AFA_F32> {
   static __device__ __forceinline__ void store(void* p, int64_t i, float x) { ((float*)p)[i] = x; }
 };
 
+// ------------------------------------------------------------------ key-shard sums
+// One element of a key shard's unnormalised sums: stored (mode 1, ACC_STORE) or added (mode 2,
+// ACC_ADD) to what the caller's array holds.
+template <typename T>
+__device__ __forceinline__ void acc_row(T* p, T x, int mode) {
+  *p = mode == 2 ? *p + x : x;
+}
+
 // ------------------------------------------------------------------ rho(s)^8
 // Two-branch, cancellation-safe evaluation (src/kernels/pallas_afa.py:39-49):
 //   t = 1 + s^2, r = rsqrt(t); s >= 0: rho = s + t r;  s < 0: rho = r / (1 - s r)

@@ -396,6 +396,32 @@ __device__ __forceinline__ void d64_body(const FwdArgs& a, D64Tile* lds_k, D64Ti
     tile_end(t);
   }
 
+  if (a.acc) {
+    // one key shard: the unnormalised sums go to the caller's fp32 arrays, stored (ACC_STORE) or
+    // added to what they hold (ACC_ADD)
+    float* op = (float*)a.out + b * a.o_b + h * a.o_h;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const float tot = rowsum[qb] + __shfl_xor(rowsum[qb], 32);
+      const int qi = q0_w + qb * 32 + l32;
+      if (qi < L) {
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            f32x4_t* p = (f32x4_t*)(op + (int64_t)qi * a.o_l + db * 32 + r4 * 8 + 4 * g);
+            f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+            if (a.acc == ACC_ADD) x = *p;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] += o[db][qb][r4 * 4 + u];
+            *p = x;
+          }
+        }
+        if (g == 0) acc_row(a.denom + (int64_t)bh * L + qi, tot, a.acc);
+      }
+    }
+    return;
+  }
   // ---- epilogue: one IEEE division per row, then products
   unsigned short* op = (unsigned short*)a.out + b * a.o_b + h * a.o_h;
 #pragma unroll

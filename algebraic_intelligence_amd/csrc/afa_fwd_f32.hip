@@ -181,6 +181,7 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
         for (int u = 0; u < 4; ++u) st = mma_f32(kv[u], qf[4 * j4 + u], st);
       }
       const bool need_mask = (a.causal && key0 + 31 > q0_w) || key0 + 31 >= vlen || q0_w + 31 >= L;
+      float ts = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         float p = rho8_exact(st[e] * scale);
@@ -190,15 +191,26 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
           p = keep ? p : 0.f;
         }
         st[e] = p;
-        dsum += p;
+        ts += p;
       }
+      // two-level sums: the tile's own (row sum and PV from zero), then added to the running
+      // ones, as the reference adds one block's dot(p, v) at a time
+      // (src/kernels/pallas_afa.py:131-139); a single chain over L keys would carry a rounding
+      // error growing with L (4.8e-6 normwise at L = 4096 against 1.3e-6 for 256-key chains)
+      dsum += ts;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+      for (int db = 0; db < NDB; ++db) {
+        f32x16_t ot;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ot[e] = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int kr = 8 * (j >> 2) + 4 * g + (j & 3);
-          o[db] = mma_f32(vt[kr * LDV + db * 32 + l32], st[j], o[db]);
+          ot = mma_f32(vt[kr * LDV + db * 32 + l32], st[j], ot);
         }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] += ot[e];
+      }
     }
     // the buffer of tile t+1 was last read in tile t-1, before the previous barrier
     if (t + 1 < ntiles) store((t + 1) & 1);
@@ -237,13 +249,23 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         if (DV == D || db * 32 + 8 * e4 + 4 * g < D) {
+          f32x4_t* p = (f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g);
           f32x4_t w;
+          if (a.acc) {
+            // one key shard: the unnormalised sums, stored or added to the caller's arrays
+            if (a.acc == ACC_ADD) w = *p;
+            else w = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u] / tot;
-          *(f32x4_t*)(op + db * 32 + 8 * e4 + 4 * g) = w;
+            for (int u = 0; u < 4; ++u) w[u] += o[db][4 * e4 + u];
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) w[u] = o[db][4 * e4 + u] / tot;
+          }
+          *p = w;
         }
       }
-    if (a.denom != nullptr && g == 0) a.denom[(int64_t)bh * L + qi] = tot;
+    if (a.acc && g == 0) acc_row(a.denom + (int64_t)bh * L + qi, dsum, a.acc);
+    else if (a.denom != nullptr && g == 0) a.denom[(int64_t)bh * L + qi] = tot;
   }
 }
 
@@ -268,6 +290,16 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_combine_kernel(const FwdArgs 
   const int bh = (int)(row / a.L), l = (int)(row % a.L);
   const int b = bh / a.H, h = bh % a.H;
   float* op = (float*)a.out + b * a.o_b + h * a.o_h + (int64_t)l * a.o_l + 4 * c4;
+  if (a.acc) {
+    // one key shard: the sums, stored or added to the caller's arrays (the sink is 0)
+    f32x4_t w = {0.f, 0.f, 0.f, 0.f};
+    if (a.acc == ACC_ADD) w = *(const f32x4_t*)op;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) w[u] += acc[u];
+    *(f32x4_t*)op = w;
+    if (c4 == 0) acc_row(a.denom + row, tot, a.acc);
+    return;
+  }
   f32x4_t w;
 #pragma unroll
   for (int u = 0; u < 4; ++u) w[u] = acc[u] / tot;

@@ -384,8 +384,8 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   // epilogue
   const float tot = rowsum + __shfl_xor(rowsum, 32) + a.omega;
   if (a.acc) {
-    // a hop of a ring / one key shard: the unnormalised sums are added to the caller's fp32
-    // accumulators (every element of this block's rows belongs to this lane alone)
+    // one key shard: the unnormalised sums go to the caller's fp32 arrays, stored (ACC_STORE) or
+    // added to what they hold (ACC_ADD); every element of this block's rows belongs to one lane
     if (qi < L) {
       float* op = (float*)a.out + b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
 #pragma unroll
@@ -394,13 +394,14 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
         for (int r4 = 0; r4 < 4; ++r4) {
           const int f = db * 32 + r4 * 8 + 4 * g;
           if (D == DP || f < D) {
-            f32x4_t x = *(const f32x4_t*)(op + f);
+            f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+            if (a.acc == ACC_ADD) x = *(const f32x4_t*)(op + f);
 #pragma unroll
             for (int u = 0; u < 4; ++u) x[u] += o[db][r4 * 4 + u] * a.w_unscale;
             *(f32x4_t*)(op + f) = x;
           }
         }
-      if (g == 0) a.denom[(int64_t)bh * L + qi] += (tot - a.omega) * a.w_unscale;
+      if (g == 0) acc_row(a.denom + (int64_t)bh * L + qi, (tot - a.omega) * a.w_unscale, a.acc);
     }
     return;
   }

@@ -214,12 +214,12 @@ __global__ __launch_bounds__(256) void afa_fwd_generic_kernel(const GenArgs a) {
     }
   }
   if (qi < a.L && a.acc) {
-    // a hop of a ring / one key shard: the unnormalised sums added to the caller's accumulators
+    // one key shard: the unnormalised sums, stored (ACC_STORE) or added to the caller's arrays
     const int64_t obase = b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
 #pragma unroll
     for (int m = 0; m < M; ++m)
-      if (sub + 8 * m < D) ((T*)a.out)[obase + sub + 8 * m] += o[m];
-    if (sub == 0) ((T*)a.denom)[(int64_t)bh * a.L + qi] += dsum;
+      if (sub + 8 * m < D) acc_row((T*)a.out + obase + sub + 8 * m, o[m], a.acc);
+    if (sub == 0) acc_row((T*)a.denom + (int64_t)bh * a.L + qi, dsum, a.acc);
   } else if (qi < a.L) {
     const T tot = dsum + (T)a.omega;
     const int64_t obase = b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;

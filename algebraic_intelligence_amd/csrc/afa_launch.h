@@ -6,6 +6,10 @@
 
 namespace afa {
 
+// Forward epilogues for one key shard (AFA_FLAG_PARTIAL, AFA_FLAG_ACCUMULATE): none (normalised
+// output), store the unnormalised sums, or add them to what the caller's arrays hold.
+enum AccMode { ACC_NONE = 0, ACC_STORE = 1, ACC_ADD = 2 };
+
 // Fused MFMA forward (afa_fwd_mfma.hip).
 struct FwdArgs {
   const void* q;
@@ -43,8 +47,8 @@ struct FwdArgs {
   int ks_items;
   float* ks_part;
   int* ks_cnt;
-  // AFA_FLAG_ACCUMULATE: out is fp32 (element strides o_*) and receives += the unnormalised
-  // numerator, denom += the row sum (sink_omega is 0)
+  // AFA_FLAG_PARTIAL / AFA_FLAG_ACCUMULATE (AccMode): out is fp32 (element strides o_*) and
+  // receives the unnormalised numerator, denom the row sum (sink_omega is 0)
   int acc;
 };
 
@@ -80,7 +84,7 @@ struct GenArgs {
   int valid_len;
   int causal;
   int exact_ref;
-  int acc;  // forward, AFA_FLAG_ACCUMULATE: out and denom (accumulation type) receive += sums
+  int acc;  // forward, AccMode: out and denom (accumulation type) receive the unnormalised sums
   double scale;
   double omega;
   // fast-rho guard of the MFMA backward (as FwdArgs): per 64-row block bounds of q (for the dK/dV

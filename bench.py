@@ -5,7 +5,8 @@
 --workload selects another configuration of BASELINE.json for the same JSON line (the default,
 c3, is the metric's own configuration): c2 (B=4 H=8 L=2048 D=64 bf16 causal), c4 / c4f32
 (B=32 H=4 L=1024 D=64 bf16 / fp32 causal, default Cayley parameters), c5 (B=2 H=16 L=8192
-D=128 bf16 causal forward) and c5bwd (its analytical backward, 10 B H D N_pairs FLOPs).
+D=128 bf16 causal forward) and c5bwd (its analytical backward, 10 B H D N_pairs FLOPs); ring16,
+c5ring8 and c3ring8 time distributed_ring_afa with its shards' hops run in turn on this GPU.
 
 Workload (C3): B=8, H=12, L=4096, D=64, bf16, causal, q/k Cayley-rotated in-kernel with
 Cayley parameters t_i = 10000^(-2i/D); q, k, v ~ N(0, 1) synthetic, resident in HBM.
@@ -105,7 +106,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--workload", default="c3",
-                    choices=sorted(WORKLOADS) + sorted(SOFTMAX_WORKLOADS) + sorted(OACE_WORKLOADS))
+                    choices=sorted(WORKLOADS) + sorted(SOFTMAX_WORKLOADS) + sorted(OACE_WORKLOADS)
+                    + sorted(RING_WORKLOADS))
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB --steps times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -297,6 +299,72 @@ def oace_bench(args, dev):
     }), flush=True)
 
 
+# Sequence ring (distributed_ring_afa) with its hops run in turn on one GPU: name -> (B, H, L, D,
+# dtype, causal, shards, description).  ring16 is the reference's 16-chip ring check
+# (scripts/run_phase6_tpu.py:358-435: B=1 H=8 L=4096 as 16 shards of 256, D=64, fp32, non-causal).
+RING_WORKLOADS = {
+    "ring16": (1, 8, 4096, 64, "fp32", False, 16, "distributed_ring_afa, the reference's 16-shard ring check"),
+    "c5ring8": (2, 16, 8192, 128, "bf16", True, 8, "distributed_ring_afa, C5 shape as 8 shards of 1024"),
+    "c3ring8": (8, 12, 4096, 64, "bf16", True, 8, "distributed_ring_afa, C3 shape (no rotary) as 8 shards of 512"),
+}
+
+
+def ring_bench(args, dev):
+    """The whole ring (accumulator clears, every hop's accumulating afa_fwd calls, the final
+    division) as one step, against one fused forward call on the same inputs.  FLOPs as the
+    forward's: 4 B H D per kept (query, key) pair, which the ring's hops cover exactly once."""
+    import torch
+
+    import algebraic_intelligence_amd as A
+
+    B, H, L, D, dt_name, causal, n, workload = RING_WORKLOADS[args.workload]
+    tdt = torch.bfloat16 if dt_name == "bf16" else torch.float32
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn((B, H, L, D), generator=g, device=dev, dtype=torch.float32).to(tdt)
+               for _ in range(3))
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+
+    def ring():
+        res["out"] = A.distributed_ring_afa(q, k, v, sink_omega=0.5, causal=causal, num_devices=n)
+
+    def full():
+        A.pallas_afa_forward(q, k, v, sink_omega=0.5, causal=causal)
+
+    def timed(step):
+        warm = warm_up(step, args)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps, warm
+
+    ms, warm = timed(ring)
+    ms_full, _ = timed(full)
+    if not torch.isfinite(res["out"].float()).all():
+        raise RuntimeError("non-finite output")
+    flops = A.afa_flops(B, H, L, D, causal=causal)
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak = PEAK_BF16_TFLOPS if dt_name == "bf16" else PEAK_FP32_TFLOPS
+    print(json.dumps({
+        "metric": f"AFA ring TFLOP/s, {n} shards on 1 GPU [{args.workload}]",
+        "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "warmup_run": {"steps": warm[0], "seconds": warm[1]},
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": dt_name, "data": f"synthetic: q,k,v ~ N(0,1) {dt_name}, resident in HBM",
+        "config": {"workload": workload, "batch": B, "heads": H, "seq_len": L, "head_dim": D, "causal": causal,
+                   "shards": n, "shard_len": L // n, "sink_omega": 0.5, "flops_per_step": flops},
+        "full_forward": {"ms": round(ms_full, 5), "tflops": round(flops / (ms_full * 1e-3) / 1e12, 3),
+                         "ring_over_full": round(ms / ms_full, 3)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": None,
+                     "duration_of": "one ring: accumulator clears, every hop's afa_fwd calls, afa_ring_finish"},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -322,6 +390,9 @@ def main():
         return
     if args.workload in OACE_WORKLOADS:
         oace_bench(args, dev)
+        return
+    if args.workload in RING_WORKLOADS:
+        ring_bench(args, dev)
         return
     B, H, L, D, dt_name, causal, rot_kind, backward, workload = WORKLOADS[args.workload]
     tdt = torch.bfloat16 if dt_name == "bf16" else torch.float32

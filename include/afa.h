@@ -56,13 +56,17 @@ enum afa_status {
                                       out = o * (1/(D+Omega)) (pallas_afa.py:283-297) */
 #define AFA_FLAG_SIMPLE_SCHEDULE 0x8u /* bf16/fp16 head_dim 64 and 128: use the non-pipelined
                                          MFMA kernel (the reference point for the pipelined ones) */
-/* afa_fwd: one hop of the ring / one key shard of distributed_ring_afa
-   (src/kernels/pallas_afa.py:618-662, _ring_step): out and denom are accumulators in the
-   accumulation type (fp32; fp64 for AFA_F64), with out's strides, and the call adds the
-   unnormalised sums to them: out += sum_j rho(s_ij)^8 v_j (rho^8 rounded to v's dtype as the
-   PV operand), denom += sum_j rho(s_ij)^8.  sink_omega must be 0 (the sink enters only the final
-   division, out / (denom + sink)) and denom must not be NULL. */
+/* afa_fwd on one key shard, as one hop of distributed_ring_afa (src/kernels/pallas_afa.py:618-662,
+   _ring_step) or one part of a split-K sum: out and denom are arrays in the accumulation type
+   (fp32; fp64 for AFA_F64), out with the strides given for it, denom contiguous (batch, heads,
+   seq_len), and they receive the unnormalised sums num_i = sum_j rho(s_ij)^8 v_j (rho^8 rounded
+   to v's dtype as the PV operand) and den_i = sum_j rho(s_ij)^8.  AFA_FLAG_PARTIAL stores them
+   (out = num, denom = den: the first hop, or a split-K part), AFA_FLAG_ACCUMULATE adds them to
+   what the arrays hold (out += num, denom += den: every later hop).  sink_omega must be 0 (the
+   sink enters only the final division, afa_ring_finish) and denom must not be NULL; the two
+   flags exclude each other. */
 #define AFA_FLAG_ACCUMULATE 0x100u
+#define AFA_FLAG_PARTIAL 0x200u
 
 const char* afa_status_string(int status);
 int afa_last_hip_error(void);
@@ -101,7 +105,7 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
 /*
  * Final step of distributed_ring_afa (src/kernels/pallas_afa.py:660-661): out = acc / (denom +
  * sink_omega), divided in the accumulation type (fp32; fp64 for AFA_F64) and rounded to dtype.
- * acc and denom are the accumulators that afa_fwd calls with AFA_FLAG_ACCUMULATE filled: acc
+ * acc and denom are the sums that afa_fwd calls with AFA_FLAG_PARTIAL / ACCUMULATE filled: acc
  * (batch, heads, seq_len, head_dim), denom contiguous (batch, heads, seq_len).  strides
  * (nullable = contiguous): 6 element strides, (b, h, l) of acc then of out; head_dim contiguous.
  */

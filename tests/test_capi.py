@@ -96,14 +96,16 @@ def test_afa_fwd_rejects_invalid_arguments(lib, kw, code):
 
 
 def test_afa_fwd_accumulate_arguments(lib):
-    """AFA_FLAG_ACCUMULATE (one hop of src/kernels/pallas_afa.py:618-662) needs the row-sum
-    accumulator and a zero sink (the sink enters only the final division); afa_ring_finish checks
-    its arguments as afa_fwd does.  Every case is refused before any device work."""
-    acc = _lib.FLAG_ACCUMULATE
-    call = lambda den, sink: lib.afa_fwd(_lib.AFA_BF16, 1, 1, 64, 64, DUMMY, DUMMY, DUMMY, None, DUMMY, den,
-                                         None, None, 0, sink, 0, 0, acc, None, 0, None)
-    assert call(None, 0.0) == _lib.ERR_NULL
-    assert call(DUMMY, 0.5) == _lib.ERR_SINK
+    """AFA_FLAG_PARTIAL / AFA_FLAG_ACCUMULATE (one hop of src/kernels/pallas_afa.py:618-662) need
+    the row-sum array and a zero sink (the sink enters only the final division) and exclude each
+    other; afa_ring_finish checks its arguments as afa_fwd does.  Every case is refused before
+    any device work."""
+    call = lambda den, sink, fl: lib.afa_fwd(_lib.AFA_BF16, 1, 1, 64, 64, DUMMY, DUMMY, DUMMY, None, DUMMY, den,
+                                             None, None, 0, sink, 0, 0, fl, None, 0, None)
+    for fl in (_lib.FLAG_ACCUMULATE, _lib.FLAG_PARTIAL):
+        assert call(None, 0.0, fl) == _lib.ERR_NULL
+        assert call(DUMMY, 0.5, fl) == _lib.ERR_SINK
+    assert call(DUMMY, 0.0, _lib.FLAG_ACCUMULATE | _lib.FLAG_PARTIAL) == _lib.ERR_UNSUPPORTED
     fin = lambda **kw: lib.afa_ring_finish(kw.get("dt", _lib.AFA_BF16), 1, 1, kw.get("L", 64), kw.get("D", 64),
                                            kw.get("acc", DUMMY), kw.get("den", DUMMY), None,
                                            kw.get("sink", 0.5), kw.get("out", DUMMY), None)
@@ -114,7 +116,7 @@ def test_afa_fwd_accumulate_arguments(lib):
     assert fin(L=0) == _lib.ERR_SHAPE
     assert fin(D=192) == _lib.ERR_HEAD_DIM
     assert fin(sink=-1.0) == _lib.ERR_SINK
-    # the accumulate plan never takes the 256-query kernel, so its key-split workspace is covered
+    # the key-shard plan never takes the fully fused kernel; its pipelined kernels' workspace is covered
     for shape in ((1, 8, 4096, 64), (16, 8, 512, 64), (3, 5, 1000, 128)):
         assert lib.afa_fwd_workspace_size(_lib.AFA_BF16, *shape, 0) > 0
 
@@ -221,7 +223,7 @@ def test_python_constants_match_the_header():
     pairs = {
         "AFA_FLAG_EXACT_TAIL": _lib.FLAG_EXACT_TAIL, "AFA_FLAG_GENERIC": _lib.FLAG_GENERIC,
         "AFA_FLAG_EXACT_REF": _lib.FLAG_EXACT_REF, "AFA_FLAG_SIMPLE_SCHEDULE": _lib.FLAG_SIMPLE_SCHEDULE,
-        "AFA_FLAG_ACCUMULATE": _lib.FLAG_ACCUMULATE,
+        "AFA_FLAG_ACCUMULATE": _lib.FLAG_ACCUMULATE, "AFA_FLAG_PARTIAL": _lib.FLAG_PARTIAL,
         "OACE_W_DV": oace.OACE_W_DV, "OACE_W_VD": oace.OACE_W_VD, "OACE_ROW_FIELDS": oace.ROW_FIELDS,
         "OACE_FLAG_WT_READY": oace.FLAG_WT_READY, "OACE_FLAG_Z_READY": oace.FLAG_Z_READY,
         "OACE_FLAG_RECOMPUTE_Z": oace.FLAG_RECOMPUTE_Z,
