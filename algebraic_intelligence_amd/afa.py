@@ -301,8 +301,9 @@ def distributed_ring_afa(
     (d - h) mod n to fp32 accumulators; out = o / (d + sink_omega) after n hops.  Here, on one
     GPU, q, k and v are the whole (B, H, L, D) arrays, L = num_devices * shard_len, device d's
     shard being rows [d * shard_len, (d + 1) * shard_len), and the result is the devices' outputs
-    side by side.  A hop is one afa_fwd call over every device's pair at once (two where the ring
-    wraps round): the devices are the batch axis of strided views, so no shard moves.  Hop 0
+    side by side.  A hop is one afa_fwd call over every device's pair at once: the devices are the
+    batch axis of strided views (non-causal: over the key/value shards stored twice in a row, so
+    that the shards a hop wraps round to follow on), and no shard moves between hops.  Hop 0
     stores the sums (AFA_FLAG_PARTIAL, so the accumulators need no clearing), every later hop adds
     to them (AFA_FLAG_ACCUMULATE).  causal: hop 0 pairs each shard with itself under the causal
     mask, and at hop h > 0 only devices d >= h hold an earlier shard; the later ones (masked whole
@@ -335,22 +336,35 @@ def distributed_ring_afa(
         stream = _lib.stream_ptr(dev)
         ws_bytes = max(L_.afa_fwd_workspace_size(dt, m, B * H, S, D, 0) for m in range(1, n + 1))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        if causal or n == 1:
+            kr, vr = kd, vd
+        else:
+            # non-causal hops wrap round the ring (device d reads shard (d - hop) mod n): with the
+            # shard sequence stored twice, shard d - hop + n sits at index d - hop + n, and every
+            # hop is one call over all devices
+            kr, vr = torch.cat((kd, kd)), torch.cat((vd, vd))
+        # the hops' views differ only in their first shard: the strides are shared and the base
+        # pointers advance by one shard per device, so each hop is one C call
+        strides = _strides(qd, kr, vr, accd)
+        qp, kp, vp, ap, dp, wp = (t.data_ptr() for t in (qd, kr, vr, accd, den, ws if ws is not None else den))
+        esz = q.element_size()
+        shard, kshard = S * D * esz, kr.stride(0) * esz
+        ashard, dshard = S * D * acc.element_size(), B * H * S * den.element_size()
+        fwd = L_.afa_fwd
 
         def hop_call(d0, d1, kv0, diag, flags=_lib.FLAG_ACCUMULATE):
             # devices d0 .. d1-1 against key/value shards kv0 .. kv0 + d1 - d0 - 1
-            m = d1 - d0
-            qs, ks, vs, os_ = qd[d0:d1], kd[kv0:kv0 + m], vd[kv0:kv0 + m], accd[d0:d1]
-            rc = L_.afa_fwd(dt, m, B * H, S, D, _lib.ptr(qs), _lib.ptr(ks), _lib.ptr(vs),
-                            _strides(qs, ks, vs, os_), _lib.ptr(os_), _lib.ptr(den[d0:d1]), None,
-                            None, 0, 0.0, int(diag), 0, flags, _lib.ptr(ws), ws_bytes, stream)
+            rc = fwd(dt, d1 - d0, B * H, S, D, qp + d0 * shard, kp + kv0 * kshard, vp + kv0 * kshard, strides,
+                     ap + d0 * ashard, dp + d0 * dshard, None, None, 0, 0.0, int(diag), 0, flags,
+                     wp if ws_bytes else None, ws_bytes, stream)
             _lib.check(rc, "afa_fwd")
 
         hop_call(0, n, 0, causal, _lib.FLAG_PARTIAL)  # every device against its own shard
         for hop in range(1, n):
-            # devices d >= hop read shard d - hop; devices d < hop read shard d - hop + n
-            hop_call(hop, n, 0, False)
-            if not causal:
-                hop_call(0, hop, n - hop, False)
+            if causal:
+                hop_call(hop, n, 0, False)  # devices d >= hop read the earlier shard d - hop
+            else:
+                hop_call(0, n, n - hop, False)  # device d reads shard d - hop + n of the doubled run
         st = (ctypes.c_int64 * 6)(S * D, L * D, D, S * D, L * D, D)
         rc = L_.afa_ring_finish(dt, n, B * H, S, D, _lib.ptr(acc), _lib.ptr(den), st, float(sink_omega),
                                 _lib.ptr(out), stream)

@@ -405,18 +405,23 @@ __device__ __forceinline__ void d64_body(const FwdArgs& a, D64Tile* lds_k, D64Ti
       const float tot = rowsum[qb] + __shfl_xor(rowsum[qb], 32);
       const int qi = q0_w + qb * 32 + l32;
       if (qi < L) {
+        // every load before the first store, so that the row's memory latencies overlap
+        f32x4_t x[2][4];
 #pragma unroll
-        for (int db = 0; db < 2; ++db) {
+        for (int db = 0; db < 2; ++db)
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
-            f32x4_t* p = (f32x4_t*)(op + (int64_t)qi * a.o_l + db * 32 + r4 * 8 + 4 * g);
-            f32x4_t x = {0.f, 0.f, 0.f, 0.f};
-            if (a.acc == ACC_ADD) x = *p;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) x[u] += o[db][qb][r4 * 4 + u];
-            *p = x;
+            x[db][r4] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if (a.acc == ACC_ADD) x[db][r4] = *(const f32x4_t*)(op + (int64_t)qi * a.o_l + db * 32 + r4 * 8 + 4 * g);
           }
-        }
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[db][r4][u] += o[db][qb][r4 * 4 + u];
+            *(f32x4_t*)(op + (int64_t)qi * a.o_l + db * 32 + r4 * 8 + 4 * g) = x[db][r4];
+          }
         if (g == 0) acc_row(a.denom + (int64_t)bh * L + qi, tot, a.acc);
       }
     }

@@ -388,17 +388,25 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
     // added to what they hold (ACC_ADD); every element of this block's rows belongs to one lane
     if (qi < L) {
       float* op = (float*)a.out + b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
+      // every load before the first store, so that the row's memory latencies overlap
+      f32x4_t x[NDB][4];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int f = db * 32 + r4 * 8 + 4 * g;
+          x[db][r4] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          if (a.acc == ACC_ADD && (D == DP || f < D)) x[db][r4] = *(const f32x4_t*)(op + f);
+        }
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int f = db * 32 + r4 * 8 + 4 * g;
           if (D == DP || f < D) {
-            f32x4_t x = {0.f, 0.f, 0.f, 0.f};
-            if (a.acc == ACC_ADD) x = *(const f32x4_t*)(op + f);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) x[u] += o[db][r4 * 4 + u] * a.w_unscale;
-            *(f32x4_t*)(op + f) = x;
+            for (int u = 0; u < 4; ++u) x[db][r4][u] += o[db][r4 * 4 + u] * a.w_unscale;
+            *(f32x4_t*)(op + f) = x[db][r4];
           }
         }
       if (g == 0) acc_row(a.denom + (int64_t)bh * L + qi, (tot - a.omega) * a.w_unscale, a.acc);

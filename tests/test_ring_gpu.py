@@ -52,6 +52,12 @@ def test_ring_bf16_padded_head_dim():
     _ring_checks((1, 2, 256, 48), torch.bfloat16, 2, True, seed=51)
 
 
+def test_ring_head_dim_off_the_vector_paths():
+    """head_dim 20: the generic kernel's hops and the element-wise finish kernel."""
+    _ring_checks((1, 2, 128, 20), torch.bfloat16, 2, True, seed=58)
+    _ring_checks((1, 2, 128, 20), torch.float32, 4, False, seed=59, tol_full=1e-5, tol_ref=1e-5)
+
+
 def test_ring_long_shards_split_keys():
     """Two shards of 4096 rows and one head: few query blocks per call, so the 128-query kernel
     splits each block's keys over several workgroups and the last part accumulates."""
