@@ -26,6 +26,7 @@ from ._lib import table_2d
 __all__ = [
     "pallas_afa_forward", "tiled_afa_forward", "exact_afa_reference", "exact_afa_with_denominator",
     "tiled_afa_backward", "pallas_afa", "algebraic_flash_attention", "distributed_ring_afa",
+    "sharded_pallas_afa",
 ]
 
 
@@ -370,6 +371,45 @@ def distributed_ring_afa(
                                 _lib.ptr(out), stream)
     _lib.check(rc, "afa_ring_finish")
     return out
+
+
+def _mesh_axes(mesh) -> dict:
+    """Axis sizes of a mesh: None (one device), a mapping {axis: size}, or an object with a
+    ``shape`` mapping (a JAX Mesh exposes its axis sizes that way)."""
+    if mesh is None:
+        return {}
+    shape = mesh if isinstance(mesh, dict) else getattr(mesh, "shape", None)
+    if not isinstance(shape, dict):
+        raise TypeError(f"mesh must be None, a mapping of axis sizes, or have a .shape mapping, got {type(mesh)}")
+    return {str(k): int(v) for k, v in shape.items()}
+
+
+def sharded_pallas_afa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    mesh=None,
+    sink_omega: float = 0.5,
+    causal: bool = False,
+    block_q: int = 128,
+    block_k: int = 128,
+) -> torch.Tensor:
+    """Batch over the mesh's 'data' axis, heads over 'fsdp' (src/kernels/pallas_afa.py:665-692).
+
+    The reference places q, k and v with NamedSharding(mesh, P("data", "fsdp", None, None)) and
+    runs the differentiable pallas_afa on every shard.  (b, h) pairs are independent, so the
+    result is pallas_afa of the whole arrays; on this one GPU every shard lives on the same device
+    and one call computes them all.  The shard shapes are checked as the placement would: batch
+    divisible by the 'data' axis size and heads by 'fsdp'.
+    """
+    axes = _mesh_axes(mesh)
+    if q.ndim == 4:
+        B, H = q.shape[0], q.shape[1]
+        if B % axes.get("data", 1) != 0:
+            raise ValueError(f"batch ({B}) must be divisible by the 'data' axis size ({axes['data']})")
+        if H % axes.get("fsdp", 1) != 0:
+            raise ValueError(f"heads ({H}) must be divisible by the 'fsdp' axis size ({axes['fsdp']})")
+    return pallas_afa(q, k, v, sink_omega=sink_omega, causal=causal, block_q=block_q, block_k=block_k)
 
 
 def afa_flops(batch: int, heads: int, seq_len: int, head_dim: int, causal: bool) -> int:

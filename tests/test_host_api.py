@@ -66,6 +66,26 @@ def test_ring_argument_checks():
         A.distributed_ring_afa(q, k, v, causal=True, num_devices=4)
 
 
+def test_sharded_argument_checks():
+    """sharded_pallas_afa (src/kernels/pallas_afa.py:665-692): batch must split over 'data' and
+    heads over 'fsdp'; the mesh is None, a mapping of axis sizes or an object with .shape; the
+    pallas_afa checks follow, and a valid call on host tensors raises."""
+    q, k, v = _qkv((4, 6, 128, 64))
+    with pytest.raises(ValueError, match="data"):
+        A.sharded_pallas_afa(q, k, v, mesh={"data": 3, "fsdp": 1, "model": 1})
+    with pytest.raises(ValueError, match="fsdp"):
+        A.sharded_pallas_afa(q, k, v, mesh={"data": 2, "fsdp": 4, "model": 1})
+    with pytest.raises(TypeError):
+        A.sharded_pallas_afa(q, k, v, mesh=[2, 3])
+    with pytest.raises(ValueError):
+        A.sharded_pallas_afa(q, k, v, mesh=None, block_q=96)
+
+    class _Mesh:
+        shape = {"data": 2, "fsdp": 3, "model": 1}
+    with pytest.raises(RuntimeError, match="GPU"):
+        A.sharded_pallas_afa(q, k, v, mesh=_Mesh(), causal=True)
+
+
 def test_algebraic_softmax_checks():
     x = torch.zeros(4, 8)
     for bad in (-0.1, math.nan, math.inf):

@@ -136,3 +136,19 @@ def test_shard_flags_store_and_add_unnormalised_sums(dtype, D, B, H, L):
         base_o, base_d = (acc0, den0) if flag == _lib.FLAG_ACCUMULATE else (0.0, 0.0)
         assert normwise(to_f64(dacc - base_d), to_f64(den[..., 0])) <= 1e-5, flag
         assert normwise(to_f64(acc - base_o), o_ref) <= tol, flag
+
+
+def test_sharded_pallas_afa_equals_pallas_afa():
+    """sharded_pallas_afa (src/kernels/pallas_afa.py:665-692) on a (data 2, fsdp 3) mesh: the same
+    output and gradients as pallas_afa on the whole arrays."""
+    q, k, v = make_qkv((2, 6, 256, 64), torch.bfloat16, seed=60)
+    qs, ks, vs = (t.clone().requires_grad_(True) for t in (q, k, v))
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = A.sharded_pallas_afa(qs, ks, vs, mesh={"data": 2, "fsdp": 3, "model": 1}, causal=True)
+    ref = A.pallas_afa(qa, ka, va, causal=True)
+    assert torch.equal(out, ref)
+    g = torch.randn_like(out)
+    out.backward(g)
+    ref.backward(g)
+    for a, b in ((qs, qa), (ks, ka), (vs, va)):
+        assert torch.equal(a.grad, b.grad)
