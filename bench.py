@@ -6,7 +6,9 @@
 c3, is the metric's own configuration): c2 (B=4 H=8 L=2048 D=64 bf16 causal), c4 / c4f32
 (B=32 H=4 L=1024 D=64 bf16 / fp32 causal, default Cayley parameters), c5 (B=2 H=16 L=8192
 D=128 bf16 causal forward) and c5bwd (its analytical backward, 10 B H D N_pairs FLOPs); ring16,
-c5ring8 and c3ring8 time distributed_ring_afa with its shards' hops run in turn on this GPU.
+c5ring8 and c3ring8 time distributed_ring_afa with its shards' hops run in turn on this GPU;
+c3hop8 and c5hop8 time one ring hop at one GPU's shard shape, c3share8 C3's per-GPU share under
+8-way batch x heads sharding.
 
 Workload (C3): B=8, H=12, L=4096, D=64, bf16, causal, q/k Cayley-rotated in-kernel with
 Cayley parameters t_i = 10000^(-2i/D); q, k, v ~ N(0, 1) synthetic, resident in HBM.
@@ -56,6 +58,8 @@ WORKLOADS = {
               "C3: AFA analytical backward (dq, dk, dv), causal, Cayley rotary"),
     "c4f32bwd": (32, 4, 1024, 64, "fp32", True, "default", True,
                  "C4 (fp32): AFA analytical backward (dq, dk, dv), causal, default Cayley rotary"),
+    "c3share8": (1, 12, 4096, 64, "bf16", True, "c3", False,
+                 "C3's share of one GPU out of 8 under batch x heads sharding: 12 of its 96 (b, h) pairs"),
 }
 # A-Softmax over the last axis of (rows, cols) scores: name -> (rows, cols, dtype, backward, description)
 SOFTMAX_WORKLOADS = {
@@ -107,7 +111,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--workload", default="c3",
                     choices=sorted(WORKLOADS) + sorted(SOFTMAX_WORKLOADS) + sorted(OACE_WORKLOADS)
-                    + sorted(RING_WORKLOADS))
+                    + sorted(RING_WORKLOADS) + sorted(HOP_WORKLOADS))
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB --steps times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -302,11 +306,73 @@ def oace_bench(args, dev):
 # Sequence ring (distributed_ring_afa) with its hops run in turn on one GPU: name -> (B, H, L, D,
 # dtype, causal, shards, description).  ring16 is the reference's 16-chip ring check
 # (scripts/run_phase6_tpu.py:358-435: B=1 H=8 L=4096 as 16 shards of 256, D=64, fp32, non-causal).
+# One ring hop at one GPU's shard shape: name -> (B, H, shard_len, D, dtype, description); one
+# afa_fwd call with AFA_FLAG_ACCUMULATE, non-causal (every hop but the diagonal one).
+HOP_WORKLOADS = {
+    "c3hop8": (8, 12, 512, 64, "bf16", "one non-causal ring hop of C3 on 8 GPUs: 512 queries x 512 keys per head"),
+    "c5hop8": (2, 16, 1024, 128, "bf16", "one non-causal ring hop of C5 on 8 GPUs: 1024 queries x 1024 keys per head"),
+}
+
 RING_WORKLOADS = {
     "ring16": (1, 8, 4096, 64, "fp32", False, 16, "distributed_ring_afa, the reference's 16-shard ring check"),
     "c5ring8": (2, 16, 8192, 128, "bf16", True, 8, "distributed_ring_afa, C5 shape as 8 shards of 1024"),
     "c3ring8": (8, 12, 4096, 64, "bf16", True, 8, "distributed_ring_afa, C3 shape (no rotary) as 8 shards of 512"),
 }
+
+
+def hop_bench(args, dev):
+    """One ring hop as one GPU of the ring runs it: afa_fwd with AFA_FLAG_ACCUMULATE on its query
+    shard and one received key/value shard, adding into fp32 accumulators resident in HBM."""
+    import torch
+
+    from algebraic_intelligence_amd import _lib
+
+    B, H, S, D, dt_name, workload = HOP_WORKLOADS[args.workload]
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn((B, H, S, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+               for _ in range(3))
+    acc = torch.zeros((B, H, S, D), dtype=torch.float32, device=dev)
+    den = torch.zeros((B, H, S), dtype=torch.float32, device=dev)
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+    wsb = lib.afa_fwd_workspace_size(_lib.AFA_BF16, B, H, S, D, 0)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    strides = (__import__("ctypes").c_int64 * 12)(*(list(q.stride()[:3]) * 3 + list(acc.stride()[:3])))
+
+    def step():
+        r = lib.afa_fwd(_lib.AFA_BF16, B, H, S, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), strides,
+                        acc.data_ptr(), den.data_ptr(), None, None, 0, 0.0, 0, 0, _lib.FLAG_ACCUMULATE,
+                        ws.data_ptr(), wsb, stream.cuda_stream)
+        if r != 0:
+            _lib.check(r, "afa_fwd")
+
+    warm = warm_up(step, args)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    flops = 4 * B * H * S * S * D
+    tflops = flops / (ms * 1e-3) / 1e12
+    # algorithmic bytes: q, k, v read; the fp32 accumulators read and written; row sums likewise
+    nbytes = 3 * B * H * S * D * 2 + 2 * B * H * S * D * 4 + 2 * B * H * S * 4
+    print(json.dumps({
+        "metric": f"AFA ring hop TFLOP/s (1 GPU's share) [{args.workload}]",
+        "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "warmup_run": {"steps": warm[0], "seconds": warm[1]}, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dt_name,
+        "data": "synthetic: q,k,v ~ N(0,1) bf16, fp32 accumulators, resident in HBM",
+        "config": {"workload": workload, "batch": B, "heads": H, "shard_len": S, "head_dim": D, "causal": False,
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "duration_of": "one afa_fwd call: the row-norm pre-pass and the hop kernel"},
+        "hbm": {"algorithmic_bytes": nbytes, "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "flop_per_byte": round(flops / nbytes, 1)},
+    }), flush=True)
 
 
 def ring_bench(args, dev):
@@ -393,6 +459,9 @@ def main():
         return
     if args.workload in RING_WORKLOADS:
         ring_bench(args, dev)
+        return
+    if args.workload in HOP_WORKLOADS:
+        hop_bench(args, dev)
         return
     B, H, L, D, dt_name, causal, rot_kind, backward, workload = WORKLOADS[args.workload]
     tdt = torch.bfloat16 if dt_name == "bf16" else torch.float32
