@@ -35,7 +35,7 @@ SIGNATURES = {
                        _dbl, _int, _i64, _uint, _vp, _sz, _vp]),
     "afa_fwd_noalloc": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                _dbl, _int, _i64, _uint, _vp]),
-    "afa_ring_finish": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _dbl, _vp, _vp]),
+    "afa_ring_finish": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _dbl, _vp, _vp, _vp]),
     "afa_bwd_workspace_size": (_sz, [_int, _i64, _i64, _i64, _i64, _int]),
     "afa_bwd": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                        _vp, _vp, _i64, _dbl, _int, _i64, _uint, _vp, _sz, _vp]),

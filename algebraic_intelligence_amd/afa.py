@@ -286,51 +286,20 @@ def _device_major(t: torch.Tensor, n: int) -> torch.Tensor:
     return t.as_strided((n, B * H, S, D), (S * D, L * D, D, 1), t.storage_offset())
 
 
-def distributed_ring_afa(
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    sink_omega: float = 0.5,
-    causal: bool = False,
-    axis_name: str = "devices",
-    num_devices: int = 16,
-) -> torch.Tensor:
-    """Ring AFA over ``num_devices`` sequence shards (src/kernels/pallas_afa.py:618-662).
-
-    The reference runs once per device inside a mesh: device d holds query shard d, the key and
-    value shards travel round the ring, and hop h adds rho(s)^8-weighted sums of shard
-    (d - h) mod n to fp32 accumulators; out = o / (d + sink_omega) after n hops.  Here, on one
-    GPU, q, k and v are the whole (B, H, L, D) arrays, L = num_devices * shard_len, device d's
-    shard being rows [d * shard_len, (d + 1) * shard_len), and the result is the devices' outputs
-    side by side.  A hop is one afa_fwd call over every device's pair at once: the devices are the
-    batch axis of strided views (non-causal: over the key/value shards stored twice in a row, so
-    that the shards a hop wraps round to follow on), and no shard moves between hops.  Hop 0
-    stores the sums (AFA_FLAG_PARTIAL, so the accumulators need no clearing), every later hop adds
-    to them (AFA_FLAG_ACCUMULATE).  causal: hop 0 pairs each shard with itself under the causal
-    mask, and at hop h > 0 only devices d >= h hold an earlier shard; the later ones (masked whole
-    in the reference) are not computed.  The accumulators are fp32 (fp64 for fp64 inputs); the
-    final division is afa_ring_finish.  ``axis_name`` is accepted for signature compatibility.
-    """
-    del axis_name
-    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
-        raise ValueError("q, k, and v must all have shape (batch, heads, sequence, dimension)")
-    if q.shape != k.shape or q.shape != v.shape:
-        raise ValueError(f"q, k, and v shapes must match, got {tuple(q.shape)}, {tuple(k.shape)}, and {tuple(v.shape)}")
-    if not _finite_nonneg(sink_omega):
-        raise ValueError("sink_omega must be finite and nonnegative")
-    n = int(num_devices)
-    B, H, L, D = q.shape
-    if n <= 0 or L % n != 0:
-        raise ValueError(f"seq_len ({L}) must split into num_devices ({num_devices}) equal shards")
+def _ring_forward(q, k, v, sink_omega, causal, n, want_total):
+    """The ring's hops and final division (see distributed_ring_afa); returns (out, d_total) with
+    d_total = row sums + sink_omega as (B, H, L, 1) in the accumulation type when asked for."""
     dev = _lib.require_device(q, k, v)
     dt = _lib.dtype_code(q.dtype)
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise TypeError(f"q, k and v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    B, H, L, D = q.shape
     S = L // n
     qd, kd, vd = (_device_major(t.contiguous(), n) for t in (q, k, v))
     acc = torch.empty((B, H, L, D), dtype=_lib.accum_dtype(q.dtype), device=dev)
     den = torch.empty((n, B * H, S), dtype=acc.dtype, device=dev)
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=dev)
+    total = torch.empty((B, H, L, 1), dtype=acc.dtype, device=dev) if want_total else None
     accd = _device_major(acc, n)
     L_ = _lib.lib()
     with torch.cuda.device(dev):
@@ -366,11 +335,76 @@ def distributed_ring_afa(
                 hop_call(hop, n, 0, False)  # devices d >= hop read the earlier shard d - hop
             else:
                 hop_call(0, n, n - hop, False)  # device d reads shard d - hop + n of the doubled run
-        st = (ctypes.c_int64 * 6)(S * D, L * D, D, S * D, L * D, D)
+        # the finish runs over the same device-major views; d_total of (device, bh, row) sits at
+        # bh * L + device * S + row of the (B, H, L) array
+        st = (ctypes.c_int64 * 9)(S * D, L * D, D, S * D, L * D, D, S, L, 1)
         rc = L_.afa_ring_finish(dt, n, B * H, S, D, _lib.ptr(acc), _lib.ptr(den), st, float(sink_omega),
-                                _lib.ptr(out), stream)
+                                _lib.ptr(out), _lib.ptr(total), stream)
     _lib.check(rc, "afa_ring_finish")
-    return out
+    return out, total
+
+
+class _RingAFA(torch.autograd.Function):
+    """distributed_ring_afa with a gradient.  The ring only re-associates the sums of the full
+    attention, so its gradient is the full attention's: the analytical tiled_afa_backward on the
+    ring's output and total denominator (src/kernels/pallas_afa.py:409-522)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, sink_omega, causal, n):
+        out, total = _ring_forward(q, k, v, sink_omega, causal, n, True)
+        ctx.save_for_backward(q, k, v, out, total)
+        ctx.cfg = (sink_omega, causal)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        q, k, v, out, total = ctx.saved_tensors
+        sink_omega, causal = ctx.cfg
+        dq, dk, dv = tiled_afa_backward(q, k, v, out, total, g, sink_omega, causal)
+        return dq, dk, dv, None, None, None
+
+
+def distributed_ring_afa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    sink_omega: float = 0.5,
+    causal: bool = False,
+    axis_name: str = "devices",
+    num_devices: int = 16,
+) -> torch.Tensor:
+    """Ring AFA over ``num_devices`` sequence shards (src/kernels/pallas_afa.py:618-662).
+
+    The reference runs once per device inside a mesh: device d holds query shard d, the key and
+    value shards travel round the ring, and hop h adds rho(s)^8-weighted sums of shard
+    (d - h) mod n to fp32 accumulators; out = o / (d + sink_omega) after n hops.  Here, on one
+    GPU, q, k and v are the whole (B, H, L, D) arrays, L = num_devices * shard_len, device d's
+    shard being rows [d * shard_len, (d + 1) * shard_len), and the result is the devices' outputs
+    side by side.  A hop is one afa_fwd call over every device's pair at once: the devices are the
+    batch axis of strided views (non-causal: over the key/value shards stored twice in a row, so
+    that the shards a hop wraps round to follow on), and no shard moves between hops.  Hop 0
+    stores the sums (AFA_FLAG_PARTIAL, so the accumulators need no clearing), every later hop adds
+    to them (AFA_FLAG_ACCUMULATE).  causal: hop 0 pairs each shard with itself under the causal
+    mask, and at hop h > 0 only devices d >= h hold an earlier shard; the later ones (masked whole
+    in the reference) are not computed.  The accumulators are fp32 (fp64 for fp64 inputs); the
+    final division is afa_ring_finish.  Differentiable, as the reference's JAX function is: the
+    gradient is the full attention's (tiled_afa_backward on the ring's output and denominator).
+    ``axis_name`` is accepted for signature compatibility.
+    """
+    del axis_name
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must all have shape (batch, heads, sequence, dimension)")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q, k, and v shapes must match, got {tuple(q.shape)}, {tuple(k.shape)}, and {tuple(v.shape)}")
+    if not _finite_nonneg(sink_omega):
+        raise ValueError("sink_omega must be finite and nonnegative")
+    n = int(num_devices)
+    L = q.shape[2]
+    if n <= 0 or L % n != 0:
+        raise ValueError(f"seq_len ({L}) must split into num_devices ({num_devices}) equal shards")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _RingAFA.apply(q, k, v, float(sink_omega), bool(causal), n)
+    return _ring_forward(q, k, v, float(sink_omega), bool(causal), n, False)[0]
 
 
 def _mesh_axes(mesh) -> dict:

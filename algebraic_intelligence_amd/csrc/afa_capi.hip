@@ -407,19 +407,21 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
 
 int afa_ring_finish(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
                     const void* acc, const void* denom, const int64_t* strides, double sink_omega,
-                    void* out, void* stream) {
+                    void* out, void* total, void* stream) {
   int rc = fwd_check(dtype, batch, heads, seq_len, head_dim);
   if (rc != AFA_OK) return rc;
   if (acc == nullptr || denom == nullptr || out == nullptr) return AFA_ERR_NULL;
   if (!finite_nonneg(sink_omega)) return AFA_ERR_SINK;
   if ((batch * heads * seq_len * head_dim + 255) / 256 >= (int64_t(1) << 31)) return AFA_ERR_SHAPE;
   afa::RingFinish r = {};
-  r.acc = acc; r.denom = denom; r.out = out;
-  const int64_t dense[6] = {heads * seq_len * head_dim, seq_len * head_dim, head_dim,
-                            heads * seq_len * head_dim, seq_len * head_dim, head_dim};
+  r.acc = acc; r.denom = denom; r.out = out; r.total = total;
+  const int64_t dense[9] = {heads * seq_len * head_dim, seq_len * head_dim, head_dim,
+                            heads * seq_len * head_dim, seq_len * head_dim, head_dim,
+                            heads * seq_len, seq_len, 1};
   const int64_t* sv = strides != nullptr ? strides : dense;
   r.a_b = sv[0]; r.a_h = sv[1]; r.a_l = sv[2];
   r.o_b = sv[3]; r.o_h = sv[4]; r.o_l = sv[5];
+  r.t_b = sv[6]; r.t_h = sv[7]; r.t_l = sv[8];
   r.B = (int)batch; r.H = (int)heads; r.L = (int)seq_len; r.D = (int)head_dim;
   r.sink = sink_omega;
   return hip_status(afa::ring_finish_launch(dtype, r, (hipStream_t)stream));

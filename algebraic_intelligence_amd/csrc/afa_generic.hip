@@ -509,9 +509,10 @@ hipError_t generic_bwd_launch(int dtype, const GenArgs& a, hipStream_t st) {
 
 // ------------------------------------------------------------------------------ ring finish
 // The final division of a ring's accumulators (src/kernels/pallas_afa.py:660-661):
-// out = acc / (denom + sink) in the accumulation type, rounded to the input dtype.  One thread
-// per output element; acc and out are strided (b, h, l, contiguous features), denom is
-// contiguous over (b, h, l).
+// out = acc / (denom + sink) in the accumulation type, rounded to the input dtype; total
+// (optional) receives denom + sink, the denominator the backward takes.  One thread per output
+// element; acc, out and total are strided (b, h, l, and contiguous features for acc and out),
+// denom is contiguous over (b, h, l).
 template <int DT>
 __global__ __launch_bounds__(256) void afa_ring_finish_kernel(const RingFinish r) {
   typedef typename Acc<DT>::T T;
@@ -524,6 +525,7 @@ __global__ __launch_bounds__(256) void afa_ring_finish_kernel(const RingFinish r
   const T d = ((const T*)r.denom)[row] + (T)r.sink;
   const T x = ((const T*)r.acc)[b * r.a_b + h * r.a_h + l * r.a_l + f];
   st<DT>(r.out, b * r.o_b + h * r.o_h + l * r.o_l + f, x / d);
+  if (r.total != nullptr && f == 0) ((T*)r.total)[b * r.t_b + h * r.t_h + l * r.t_l] = d;
 }
 
 // The same with 8 features per thread and 16-byte loads and stores (head_dim a multiple of 8,
@@ -542,6 +544,7 @@ __global__ __launch_bounds__(256) void afa_ring_finish_vec_kernel(const RingFini
   const int64_t bh = row / r.L, l = row - bh * r.L;
   const int64_t b = bh / r.H, h = bh - b * r.H;
   const T d = ((const T*)r.denom)[row] + (T)r.sink;
+  if (r.total != nullptr && c == 0) ((T*)r.total)[b * r.t_b + h * r.t_h + l * r.t_l] = d;
   const T* src = (const T*)r.acc + b * r.a_b + h * r.a_h + l * r.a_l + c;
   const int64_t o = b * r.o_b + h * r.o_h + l * r.o_l + c;
   T x[8];

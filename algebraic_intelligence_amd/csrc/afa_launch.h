@@ -167,7 +167,8 @@ struct RingFinish {
   const void* acc;    // fp32 (fp64 for AFA_F64) numerators
   const void* denom;  // row sums, contiguous over (b, h, l)
   void* out;          // the input dtype
-  int64_t a_b, a_h, a_l, o_b, o_h, o_l;
+  void* total;        // nullable: denom + sink in the accumulation type, strides t_*
+  int64_t a_b, a_h, a_l, o_b, o_h, o_l, t_b, t_h, t_l;
   int B, H, L, D;
   double sink;
 };

@@ -106,12 +106,14 @@ int afa_fwd(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t he
  * Final step of distributed_ring_afa (src/kernels/pallas_afa.py:660-661): out = acc / (denom +
  * sink_omega), divided in the accumulation type (fp32; fp64 for AFA_F64) and rounded to dtype.
  * acc and denom are the sums that afa_fwd calls with AFA_FLAG_PARTIAL / ACCUMULATE filled: acc
- * (batch, heads, seq_len, head_dim), denom contiguous (batch, heads, seq_len).  strides
- * (nullable = contiguous): 6 element strides, (b, h, l) of acc then of out; head_dim contiguous.
+ * (batch, heads, seq_len, head_dim), denom contiguous (batch, heads, seq_len).  total (nullable)
+ * receives denom + sink_omega in the accumulation type: the d_total that afa_bwd takes, so the
+ * ring's gradient is afa_bwd's.  strides (nullable = contiguous): 9 element strides, (b, h, l) of
+ * acc, of out, then of total; head_dim contiguous.
  */
 int afa_ring_finish(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
                     const void* acc, const void* denom, const int64_t* strides, double sink_omega,
-                    void* out, void* stream);
+                    void* out, void* total, void* stream);
 
 /*
  * afa_fwd without allocation.  No counterpart in the reference: for callers that cannot allocate

@@ -108,7 +108,7 @@ def test_afa_fwd_accumulate_arguments(lib):
     assert call(DUMMY, 0.0, _lib.FLAG_ACCUMULATE | _lib.FLAG_PARTIAL) == _lib.ERR_UNSUPPORTED
     fin = lambda **kw: lib.afa_ring_finish(kw.get("dt", _lib.AFA_BF16), 1, 1, kw.get("L", 64), kw.get("D", 64),
                                            kw.get("acc", DUMMY), kw.get("den", DUMMY), None,
-                                           kw.get("sink", 0.5), kw.get("out", DUMMY), None)
+                                           kw.get("sink", 0.5), kw.get("out", DUMMY), None, None)
     assert fin(dt=9) == _lib.ERR_DTYPE
     assert fin(acc=None) == _lib.ERR_NULL
     assert fin(den=None) == _lib.ERR_NULL

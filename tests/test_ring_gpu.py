@@ -152,3 +152,37 @@ def test_sharded_pallas_afa_equals_pallas_afa():
     ref.backward(g)
     for a, b in ((qs, qa), (ks, ka), (vs, va)):
         assert torch.equal(a.grad, b.grad)
+
+
+def test_ring_reference_test_configuration_fp64():
+    """The reference's ring test (tests/test_pallas_afa.py:227-271): fp64, B=1 H=2 L=256 D=32 as 4
+    shards, non-causal, sink 0.5; max error / max|exact| <= 1e-6 against exact_afa_reference
+    (here: against this build's exact reference and the float64 oracle, <= 1e-12)."""
+    q, k, v = make_qkv((1, 2, 256, 32), torch.float64, seed=107)
+    out = to_f64(A.distributed_ring_afa(q, k, v, sink_omega=0.5, causal=False, num_devices=4))
+    exact = to_f64(A.exact_afa_reference(q, k, v, sink_omega=0.5))
+    assert normwise(out, exact) <= 1e-6
+    assert normwise(out, O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, False)) <= 1e-12
+
+
+@pytest.mark.parametrize("dtype,causal,n", [(torch.bfloat16, True, 4), (torch.bfloat16, False, 8),
+                                            (torch.float32, True, 2), (torch.float64, False, 4)])
+def test_ring_gradients(dtype, causal, n):
+    """distributed_ring_afa is differentiable, as the reference's JAX function: its gradients equal
+    pallas_afa's on the same inputs (same analytical backward, the ring's own output and total
+    denominator), and the fp64 case matches the oracle's finite-difference-pinned backward."""
+    q, k, v = make_qkv((1, 2, 256, 64), dtype, seed=61, scale=0.5 if dtype == torch.float16 else 1.0)
+    g = make_qkv((1, 2, 256, 64), dtype, seed=62)[0]
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    A.distributed_ring_afa(qr, kr, vr, causal=causal, num_devices=n).backward(g)
+    A.pallas_afa(qa, ka, va, causal=causal).backward(g)
+    tol = {torch.bfloat16: 2e-2, torch.float32: 1e-5, torch.float64: 1e-12}[dtype]
+    for a, b, name in ((qr, qa, "dq"), (kr, ka, "dk"), (vr, va, "dv")):
+        e = normwise(to_f64(a.grad), to_f64(b.grad))
+        print(f"ring grad {dtype} causal={causal} n={n} {name}: {e:.2e}", flush=True)
+        assert e <= tol, name
+    if dtype == torch.float64:
+        dq, dk, dv = O.afa_backward(to_f64(q), to_f64(k), to_f64(v), to_f64(g), 0.5, causal)
+        for a, ref in ((qr, dq), (kr, dk), (vr, dv)):
+            assert normwise(to_f64(a.grad), ref) <= 1e-10
