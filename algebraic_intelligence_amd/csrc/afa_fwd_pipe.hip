@@ -323,16 +323,77 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
 #pragma unroll
       for (int db = 0; db < NDB; ++db) o[db] = mma16<DT>(vf[db][kk], pk[kk], o[db]);
   };
+  // The same unit where it is known to be one of the wave's units, to have a next one and to
+  // need no mask: no branch and no select in its VALU stream (the guarded form's mask test is
+  // if-converted into a compare and a select per score).
+  auto clean_unit = [&](int u, f32x16_t& scur, f32x16_t& snxt) {
+    read_kf(u + 1);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) snxt[e] = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < NK; ++kc) snxt = mma16<DT>(kf[kc], qf[kc], snxt);
+    __builtin_amdgcn_sched_barrier(0);
+    float p[16];
+    if constexpr (FAST) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = SM == 2 ? scur[r] * a.s_mult : scur[r];
+        p[r] = SM == 1 ? rho8_fast_half(x) : rho8_fast(x);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = SM == 2 ? scur[r] * a.s_mult : scur[r];
+        p[r] = SM == 1 ? rho8_exact_half(x) : rho8_exact(x);
+      }
+    }
+    rowsum += tree16x(p);
+    u32x4_t pk[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pk[kk][e] = Elem<DT>::pack(p[kk * 8 + 2 * e], p[kk * 8 + 2 * e + 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    read_vf(u);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db] = mma16<DT>(vf[db][kk], pk[kk], o[db]);
+  };
 
-  for (int u = t_lo; u < t_hi; ++u) {
-    // own loads of tile u+1 done (those of later tiles may remain), then publish them; the
-    // barrier also ends every wave's unit u-1, the last reader of the buffer reused below
+  // Step u: own loads of tile u+1 done (those of later tiles may remain), then publish them; the
+  // barrier also ends every wave's unit u-1, the last reader of the buffer reused by the issue.
+  auto step = [&](int u) {
     if (u + 2 < t_hi) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS * (NB - 3)));
     else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
     if (u + NB - 1 < t_hi) issue_tile(u + NB - 1);
-    if (u & 1) unit(u, sB, sA);
-    else unit(u, sA, sB);
+  };
+  // Units are taken in pairs from the even t_lo, so S(u) sits in sA for even u and in sB for
+  // odd u with no register copies.  Unit u is clean when u + 1 < U (a next unit exists) and no
+  // key of it needs a mask; both can only turn false as u grows, so the clean units are a prefix
+  // [t_lo, uc) of the wave's.  The loop bounds differ between waves, but every wave runs one
+  // step, and so one barrier, per tile of [t_lo, t_hi).
+  auto clean = [&](int u) {
+    const int key0 = u * KT;
+    return u + 1 < U && !((a.causal && key0 + 31 > q0_w) || key0 + 31 >= vlen);
+  };
+  int uc = t_lo;
+  while (uc < t_hi && clean(uc)) ++uc;
+  int u = t_lo;
+  for (; u + 1 < uc; u += 2) {
+    step(u);
+    clean_unit(u, sA, sB);
+    step(u + 1);
+    clean_unit(u + 1, sB, sA);
+  }
+  for (; u < t_hi; u += 2) {
+    step(u);
+    unit(u, sA, sB);
+    if (u + 1 < t_hi) {
+      step(u + 1);
+      unit(u + 1, sB, sA);
+    }
   }
 
   // key split: every part stores its fp32 partial numerators and row sums, then counts itself
