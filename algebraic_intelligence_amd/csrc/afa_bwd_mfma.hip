@@ -276,7 +276,11 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) dq[fb][e] = 0.f;
 
-  auto issue = [&](int t) {
+  auto issue = [&](int tile_index) {
+    // the tile index is the same in every lane (a loop counter of uniform bounds); stating it
+    // keeps the LDS address of the DMA in a scalar register (M0) where the compiler's uniformity
+    // analysis loses track of it inside the rho^8-form branch
+    const int t = __builtin_amdgcn_readfirstlane(tile_index);
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i;               // LDS chunk slot
@@ -302,62 +306,83 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) issue(t + 1);
-    const unsigned short* tk = lds_k[t & 1];
-    const unsigned short* tv = lds_v[t & 1];
+  // key sub-tile n of the wave's queries needs a mask (causal diagonal, valid length, rows past L)
+  auto need_mask = [&](int n) {
+    return (a.causal && n * 32 + 31 > q0_w) || n * 32 + 31 >= vlen || q0_w + 31 >= L;
+  };
+  // one 32-key sub-tile n (sub within LDS tile tk / tv) in the rho^8 form E (two-branch) or not,
+  // CLEAN (known live and unmasked: no tests, no selects) or guarded
+  auto sub_tile = [&](const unsigned short* tk, const unsigned short* tv, int sub, int n, auto exact_tag,
+                      auto clean_tag) {
+    constexpr bool E = decltype(exact_tag)::value;
+    constexpr bool CLEAN = decltype(clean_tag)::value;
+    const int rk = sub * 32 + l32;
+    f32x16_t S, P;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int n = 2 * t + sub;
-      if (n < nsub) {
-        const int rk = sub * 32 + l32;
-        f32x16_t S, P;
+    for (int e = 0; e < 16; ++e) {
+      S[e] = 0.f;
+      P[e] = 0.f;
+    }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          S[e] = 0.f;
-          P[e] = 0.f;
-        }
+    for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tk, rk, 2 * kc + g), qf[kc], S);
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tk, rk, 2 * kc + g), qf[kc], S);
+    for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<DP>(tv, rk, 2 * kc + g), gf[kc], P);
+    float ds[16];
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<DP>(tv, rk, 2 * kc + g), gf[kc], P);
-        const bool need_mask = (a.causal && n * 32 + 31 > q0_w) || n * 32 + 31 >= vlen || q0_w + 31 >= L;
-        float ds[16];
-        auto dscore = [&](auto exact_tag) {
-          constexpr bool E = decltype(exact_tag)::value;
+    for (int r = 0; r < 16; ++r) {
+      const float s = S[r] * SQ;
+      float rr;
+      const float w = rho8r<E>(s, rr) * invd;
+      ds[r] = C8 * rr * w * (P[r] - ei);
+    }
+    if (!CLEAN && need_mask(n)) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float s = S[r] * SQ;
-            float rr;
-            const float w = rho8r<E>(s, rr) * invd;
-            ds[r] = C8 * rr * w * (P[r] - ei);
-          }
-        };
-        if (fast) dscore(std::false_type{});
-        else dscore(std::true_type{});
-        if (need_mask) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int j = n * 32 + (r >> 2) * 8 + 4 * g + (r & 3);
-            const bool keep = j < vlen && qi < L && (!a.causal || j <= qi);
-            ds[r] = keep ? ds[r] : 0.f;
-          }
-        }
-        u32x4_t dsp[2];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) dsp[kk][e] = Elem<DT>::pack(ds[kk * 8 + 2 * e], ds[kk * 8 + 2 * e + 1]);
-#pragma unroll
-        for (int fb = 0; fb < NFB; ++fb)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk)
-            dq[fb] = bmma<DT>(frag_tr<DP>(tk, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dq[fb]);
+      for (int r = 0; r < 16; ++r) {
+        const int j = n * 32 + (r >> 2) * 8 + 4 * g + (r & 3);
+        const bool keep = j < vlen && qi < L && (!a.causal || j <= qi);
+        ds[r] = keep ? ds[r] : 0.f;
       }
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    __syncthreads();
-  }
+    u32x4_t dsp[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dsp[kk][e] = Elem<DT>::pack(ds[kk * 8 + 2 * e], ds[kk * 8 + 2 * e + 1]);
+#pragma unroll
+    for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        dq[fb] = bmma<DT>(frag_tr<DP>(tk, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dq[fb]);
+  };
+  // The tile loops in one rho^8 form.  Tile t is clean when both its sub-tiles are the wave's and
+  // need no mask; both tests only turn false as t grows, so the clean tiles are a prefix [0, tc)
+  // with a loop of its own (one loop holding both bodies spills).  Every wave passes ntiles
+  // barriers.
+  auto run = [&](auto exact_tag) {
+    int tc = 0;
+    // at DP = 256 (one wave per SIMD, accumulators in AGPRs) a second loop body spills
+    if constexpr (DP <= 128)
+      while (tc < ntiles && 2 * tc + 1 < nsub && !need_mask(2 * tc + 1)) ++tc;
+    if constexpr (DP <= 128) {
+      for (int t = 0; t < tc; ++t) {
+        if (t + 1 < ntiles) issue(t + 1);
+        sub_tile(lds_k[t & 1], lds_v[t & 1], 0, 2 * t, exact_tag, std::true_type{});
+        sub_tile(lds_k[t & 1], lds_v[t & 1], 1, 2 * t + 1, exact_tag, std::true_type{});
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        __syncthreads();
+      }
+    }
+    for (int t = tc; t < ntiles; ++t) {
+      if (t + 1 < ntiles) issue(t + 1);
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+        if (2 * t + sub < nsub) sub_tile(lds_k[t & 1], lds_v[t & 1], sub, 2 * t + sub, exact_tag, std::false_type{});
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      __syncthreads();
+    }
+  };
+  if (fast) run(std::false_type{});
+  else run(std::true_type{});
 
   if (qi < L) {
     if (a.rc != nullptr) {  // q was rotated: dq = R^T (dL/d(Rq))
@@ -414,6 +439,9 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
   constexpr int CPT = QT * NCK / 256;
   constexpr int NKC = DP / 16;
   constexpr int NFB = DP / 32;
+  // clean tiles (their own loop, no per-score mask) where the registers allow: at DP = 128 the
+  // guarded loop alone takes 244-248 VGPRs and a second loop body spills
+  constexpr bool CLEAN_TILES = DP < 128;
   const float SQ = score_factor<D>(a);
   const float C8 = SQ;
   const int tid = threadIdx.x;
@@ -480,71 +508,178 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
 
-  for (int t = t0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) issue(t + 1);
-    const unsigned short* tq = lds_q[t & 1];
-    const unsigned short* tg = lds_g[t & 1];
-    const float* tei = lds_ei[t & 1];
+  if constexpr (CLEAN_TILES) {
+    // Query tile t in the form CLEAN (every sub-tile live and unmasked: no tests, no selects) or
+    // guarded.  The clean tiles are a range [ta, tb): past the causal diagonal (first query row at
+    // least the wave's last key) and before the tile that reaches past L; none when the wave's
+    // keys reach the valid length.  Each range has a loop of its own (one loop holding both
+    // bodies spills); every wave passes one barrier per tile of [t0, ntiles).
+    auto tile = [&](int t, auto clean_tag) {
+      constexpr bool CLEAN = decltype(clean_tag)::value;
+      const unsigned short* tq = lds_q[t & 1];
+      const unsigned short* tg = lds_g[t & 1];
+      const float* tei = lds_ei[t & 1];
 #pragma unroll
-    for (int sub = 0; sub < SUBS; ++sub) {
-      const int m = SUBS * t + sub;                   // query sub-tile
-      const bool live = wave_live && m * 32 < L && (!a.causal || m * 32 + 31 >= k0_w);
-      if (live) {
-        const int rq = sub * 32 + l32;
-        f32x16_t S, P;
+      for (int sub = 0; sub < SUBS; ++sub) {
+        const int m = SUBS * t + sub;                   // query sub-tile
+        const bool live = CLEAN || (wave_live && m * 32 < L && (!a.causal || m * 32 + 31 >= k0_w));
+        if (live) {
+          const int rq = sub * 32 + l32;
+          f32x16_t S, P;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          S[e] = 0.f;
-          P[e] = 0.f;
-        }
+          for (int e = 0; e < 16; ++e) {
+            S[e] = 0.f;
+            P[e] = 0.f;
+          }
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
+          for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) {
-          const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
-          P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vk, P);
-        }
-        // W and dS, masked and packed to the element type four rows at a time (only those four
-        // fp32 pairs are live next to the accumulators)
-        const bool need_mask = (a.causal && m * 32 < k0_w + 31) || k0_w + 31 >= vlen || m * 32 + 31 >= L;
-        u32x4_t wp[2], dsp[2];
+          for (int kc = 0; kc < NKC; ++kc) {
+            const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
+            P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vk, P);
+          }
+          // W and dS, masked and packed to the element type four rows at a time (only those four
+          // fp32 pairs are live next to the accumulators)
+          const bool need_mask =
+              !CLEAN && ((a.causal && m * 32 < k0_w + 31) || k0_w + 31 >= vlen || m * 32 + 31 >= L);
+          u32x4_t wp[2], dsp[2];
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int lr = sub * 32 + r4 * 8 + 4 * g;  // tile row of element 4 r4
-          const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
-          const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
-          float w[4], ds[4];
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int lr = sub * 32 + r4 * 8 + 4 * g;  // tile row of element 4 r4
+            const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
+            const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
+            float w[4], ds[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int r = 4 * r4 + u;
-            const float s = S[r] * SQ;
-            float rr;
-            w[u] = rho8r<!FAST>(s, rr) * i4[u];
-            ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
-            if (need_mask) {
-              const int i = m * 32 + r4 * 8 + 4 * g + u;
-              const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
-              w[u] = keep ? w[u] : 0.f;
-              ds[u] = keep ? ds[u] : 0.f;
+            for (int u = 0; u < 4; ++u) {
+              const int r = 4 * r4 + u;
+              const float s = S[r] * SQ;
+              float rr;
+              w[u] = rho8r<!FAST>(s, rr) * i4[u];
+              ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+              if (need_mask) {
+                const int i = m * 32 + r4 * 8 + 4 * g + u;
+                const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
+                w[u] = keep ? w[u] : 0.f;
+                ds[u] = keep ? ds[u] : 0.f;
+              }
             }
+            // element r = 4 r4 + u sits in wp[r >> 3][(r & 7) >> 1]
+            wp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(w[0], w[1]);
+            wp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(w[2], w[3]);
+            dsp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(ds[0], ds[1]);
+            dsp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(ds[2], ds[3]);
+            // keep the four-row groups apart, so only one group's fp32 values are live at a time
+            if constexpr (CLEAN) __builtin_amdgcn_sched_barrier(0);
           }
-          // element r = 4 r4 + u sits in wp[r >> 3][(r & 7) >> 1]
-          wp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(w[0], w[1]);
-          wp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(w[2], w[3]);
-          dsp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(ds[0], ds[1]);
-          dsp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(ds[2], ds[3]);
+#pragma unroll
+          for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+              dv[fb] = bmma<DT>(frag_tr<DP>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
+              dk[fb] = bmma<DT>(frag_tr<DP>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
+            }
         }
-#pragma unroll
-        for (int fb = 0; fb < NFB; ++fb)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            dv[fb] = bmma<DT>(frag_tr<DP>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
-            dk[fb] = bmma<DT>(frag_tr<DP>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
-          }
       }
+    };
+    auto step_end = [&]() {
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      __syncthreads();
+    };
+    // the clean body apart from the next tile's load issue, as the guarded body's branches keep it
+    auto clean_tile = [&](int t) {
+      __builtin_amdgcn_sched_barrier(0);
+      tile(t, std::true_type{});
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int ta = t0, tb = t0;
+    if (wave_live && k0_w + 31 < vlen) {
+      ta = a.causal ? max(t0, (k0_w + 31 + QT - 1) / QT) : t0;
+      tb = max(ta, L / QT);
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    __syncthreads();
+    int t = t0;
+    for (; t < ta; ++t) {
+      if (t + 1 < ntiles) issue(t + 1);
+      tile(t, std::false_type{});
+      step_end();
+    }
+    for (; t < tb; ++t) {
+      if (t + 1 < ntiles) issue(t + 1);
+      clean_tile(t);
+      step_end();
+    }
+    for (; t < ntiles; ++t) {
+      if (t + 1 < ntiles) issue(t + 1);
+      tile(t, std::false_type{});
+      step_end();
+    }
+  } else {
+    for (int t = t0; t < ntiles; ++t) {
+      if (t + 1 < ntiles) issue(t + 1);
+      const unsigned short* tq = lds_q[t & 1];
+      const unsigned short* tg = lds_g[t & 1];
+      const float* tei = lds_ei[t & 1];
+#pragma unroll
+      for (int sub = 0; sub < SUBS; ++sub) {
+        const int m = SUBS * t + sub;                   // query sub-tile
+        const bool live = wave_live && m * 32 < L && (!a.causal || m * 32 + 31 >= k0_w);
+        if (live) {
+          const int rq = sub * 32 + l32;
+          f32x16_t S, P;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            S[e] = 0.f;
+            P[e] = 0.f;
+          }
+#pragma unroll
+          for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
+#pragma unroll
+          for (int kc = 0; kc < NKC; ++kc) {
+            const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
+            P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vk, P);
+          }
+          // W and dS, masked and packed to the element type four rows at a time (only those four
+          // fp32 pairs are live next to the accumulators)
+          const bool need_mask = (a.causal && m * 32 < k0_w + 31) || k0_w + 31 >= vlen || m * 32 + 31 >= L;
+          u32x4_t wp[2], dsp[2];
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int lr = sub * 32 + r4 * 8 + 4 * g;  // tile row of element 4 r4
+            const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
+            const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
+            float w[4], ds[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int r = 4 * r4 + u;
+              const float s = S[r] * SQ;
+              float rr;
+              w[u] = rho8r<!FAST>(s, rr) * i4[u];
+              ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+              if (need_mask) {
+                const int i = m * 32 + r4 * 8 + 4 * g + u;
+                const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
+                w[u] = keep ? w[u] : 0.f;
+                ds[u] = keep ? ds[u] : 0.f;
+              }
+            }
+            // element r = 4 r4 + u sits in wp[r >> 3][(r & 7) >> 1]
+            wp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(w[0], w[1]);
+            wp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(w[2], w[3]);
+            dsp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(ds[0], ds[1]);
+            dsp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(ds[2], ds[3]);
+          }
+#pragma unroll
+          for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+              dv[fb] = bmma<DT>(frag_tr<DP>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
+              dk[fb] = bmma<DT>(frag_tr<DP>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
+            }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      __syncthreads();
+    }
+
   }
 
   if (kj < L) {
