@@ -332,6 +332,8 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
     for (int e = 0; e < 16; ++e) snxt[e] = 0.f;
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) snxt = mma16<DT>(kf[kc], qf[kc], snxt);
+    // V(u)'s fragments are read here, so their LDS latency runs under the rho^8 chain
+    read_vf(u);
     __builtin_amdgcn_sched_barrier(0);
     float p[16];
     if constexpr (FAST) {
@@ -354,7 +356,6 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
 #pragma unroll
       for (int e = 0; e < 4; ++e) pk[kk][e] = Elem<DT>::pack(p[kk * 8 + 2 * e], p[kk * 8 + 2 * e + 1]);
     __builtin_amdgcn_sched_barrier(0);
-    read_vf(u);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
