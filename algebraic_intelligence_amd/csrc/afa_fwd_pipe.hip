@@ -90,7 +90,7 @@ __device__ __forceinline__ float tree16x(const float (&p)[16]) {
 
 template <int D>
 __device__ __forceinline__ int v_swizzle(int r, int c) {
-  if constexpr (D == 128) return c ^ ((r & 3) << 1);
+  if constexpr (D == 128) return c ^ ((r & 3) << 2);
   else return c ^ (((r >> 1) & 1) << 2);
 }
 
