@@ -158,7 +158,8 @@ using PipeTile = unsigned short[32 * DP];
 
 // Direct global -> LDS loads of key tile t (32 keys of K and of V) of one head into ring buffer
 // t % NB: slot s = tid + 256 i covers row s / CH, physical chunk s % CH; K chunk c of row r goes to
-// c ^ (r & 7), V chunk c to v_swizzle; rows past L read row L - 1 (finite data, masked keys).
+// c ^ (r mod CH) (every chunk position of the row in turn), V chunk c to v_swizzle; rows past L
+// read row L - 1 (finite data, masked keys).
 template <int D>
 __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padded_dim(D)>* lds_k,
                                                 PipeTile<padded_dim(D)>* lds_v, const unsigned short* kp,
@@ -177,7 +178,7 @@ __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padde
   for (int i = 0; i < LPT; ++i) {
     const int s = tid + 256 * i, r = s / CH, pc = s % CH;
     const int key = min(t * KT + r, a.L - 1);
-    const int lk = pc ^ (r & 7), lv = v_swizzle<DP>(r, pc);
+    const int lk = pc ^ (r & (CH - 1)), lv = v_swizzle<DP>(r, pc);
     // byte offsets within the head fit 32 bits (checked by the caller): a uniform base plus a
     // 32-bit lane offset per load
     const void* ks = (const void*)((const char*)kp + (uint32_t)(key * (int)a.k_l + lk * 8) * 2u);
@@ -231,7 +232,7 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   auto read_kf = [&](int u) {
     const unsigned short* base = &lds_k[u % NB][l32 * DP];
 #pragma unroll
-    for (int kc = 0; kc < NK; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & 7)) * 8));
+    for (int kc = 0; kc < NK; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & (CH - 1))) * 8));
   };
   auto read_vf = [&](int u) {
     const unsigned short* tile = lds_v[u % NB];
