@@ -59,11 +59,23 @@ __device__ __forceinline__ u32x4_t bscale(u32x4_t w, float sc) {
   return r;
 }
 
+// XOR key of row r's 16-byte chunks in a swizzled tile of D-element rows: chunk c of row r sits
+// at position c ^ key.  At D = 128 (256-byte rows, one full period of the LDS banks) the key
+// takes all 16 values over 16 rows, so a row fragment read (32 rows, one chunk each) uses every
+// bank, and it sends the 8 rows of a transposed read (4 consecutive chunks each) to 4 different
+// 4-chunk groups, two rows each; at D = 64 two rows share a bank period and r & 7 does both.
+template <int D>
+__device__ __forceinline__ int swz_key(int r) {
+  if constexpr (D == 128) return (r & 15) ^ ((r & 3) << 2);
+  else return r & 7;
+}
+
 // Element offset of 16-byte chunk `c` of row `r` in a swizzled tile of D-element rows.
 template <int D>
 __device__ __forceinline__ int swz(int r, int c) {
+  if constexpr (D == 128) return r * D + ((c ^ swz_key<D>(r)) << 3);
   // (c & ~7) is a compile-time constant at every call, so chunks 8 apart share one lane offset
-  return r * D + ((((c & 7) ^ (r & 7)) | (c & ~7)) << 3);
+  else return r * D + ((((c & 7) ^ (r & 7)) | (c & ~7)) << 3);
 }
 
 // Row fragment: 8 elements (chunk c) of row r.
@@ -286,7 +298,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       const int c = tid + 256 * i;               // LDS chunk slot
       const int row = c / NCK, pc = c % NCK;
       const int key = min(t * KT + row, L - 1);
-      const int lc = pc ^ (row & 7);
+      const int lc = pc ^ swz_key<DP>(row);
       unsigned short* kd = &lds_k[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* vd = &lds_v[t & 1][(256 * i + wave * 64) * 8];
       // byte offset within the head (L * D < 2^31, mfma_bwd_supported): a uniform base plus a
@@ -482,7 +494,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       const int c = tid + 256 * i;
       const int row = c / NCK, pc = c % NCK;
       const int qrow = min(t * QT + row, L - 1);
-      const int lc = pc ^ (row & 7);
+      const int lc = pc ^ swz_key<DP>(row);
       unsigned short* qd = &lds_q[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* gd = &lds_g[t & 1][(256 * i + wave * 64) * 8];
       const uint32_t off = (uint32_t)(qrow * D + lc * 8) * 2u;
@@ -769,7 +781,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       const int c = tid + 256 * i;
       const int row = c / NCK, pc = c % NCK;
       const int key = min(k0_wg + row, L - 1);
-      const int lc = pc ^ (row & 7);
+      const int lc = pc ^ swz_key<DP>(row);
       const void* vs = (const void*)((const char*)vp + (uint32_t)(key * D + lc * 8) * 2u);
       if constexpr (D < DP) {
         if (lc >= D / 8) vs = (const void*)afa_bwd_zero_chunk;
