@@ -568,7 +568,13 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
               float rr;
               w[u] = rho8r<!FAST>(s, rr) * i4[u];
               ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
-              if (need_mask) {
+            }
+            if (need_mask) {
+              // a side effect the compiler cannot move keeps this a branch on the wave-uniform
+              // need_mask instead of a compare and two selects per score in every tile
+              asm volatile("" ::: "memory");
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
                 const int i = m * 32 + r4 * 8 + 4 * g + u;
                 const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
                 w[u] = keep ? w[u] : 0.f;
@@ -666,7 +672,13 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
               float rr;
               w[u] = rho8r<!FAST>(s, rr) * i4[u];
               ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
-              if (need_mask) {
+            }
+            if (need_mask) {
+              // a side effect the compiler cannot move keeps this a branch on the wave-uniform
+              // need_mask instead of a compare and two selects per score in every tile
+              asm volatile("" ::: "memory");
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
                 const int i = m * 32 + r4 * 8 + 4 * g + u;
                 const bool keep = kj < vlen && i < L && (!a.causal || kj <= i);
                 w[u] = keep ? w[u] : 0.f;
