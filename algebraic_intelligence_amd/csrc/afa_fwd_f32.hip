@@ -98,33 +98,49 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
     qf[j + 1] = x1;
   }
 
-  // tile staging in registers: K as rotation pairs, V as float4
+  // tile staging in registers: K as rotation pairs, V as float4.  Each thread's elements sit at
+  // the same offsets in every tile: those offsets are formed once, and a tile only moves the
+  // (wave-uniform) base pointers by KT rows.
   float kx[KJOBS][2];
   float kc[KJOBS], ksn[KJOBS];
   f32x4_t vx[VJOBS];
+  int64_t koff[KJOBS], voff[VJOBS];
+  int krow[KJOBS], vrow[VJOBS], toff[KJOBS];
+#pragma unroll
+  for (int i = 0; i < KJOBS; ++i) {
+    const int e = tid + 256 * i, r = e / (D / 2), p = e % (D / 2);
+    krow[i] = r;
+    koff[i] = (int64_t)r * a.k_l + 2 * p;
+    toff[i] = r * (D / 2) + p;
+  }
+#pragma unroll
+  for (int i = 0; i < VJOBS; ++i) {
+    const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
+    vrow[i] = e < KT * (D / 4) ? r : KT;  // past the tile: never loaded
+    voff[i] = (int64_t)r * a.v_l + 4 * c4;
+  }
   auto load = [&](int t) {
+    const int rows = L - t * KT;  // rows of tile t inside the sequence
+    const float* kt = kp + (int64_t)t * KT * a.k_l;
+    const float* vt = vp + (int64_t)t * KT * a.v_l;
 #pragma unroll
     for (int i = 0; i < KJOBS; ++i) {
-      const int e = tid + 256 * i, r = e / (D / 2), p = e % (D / 2);
-      const int key = t * KT + r;
       kx[i][0] = kx[i][1] = 0.f;
       kc[i] = 1.f;
       ksn[i] = 0.f;
-      if (key < L) {
-        kx[i][0] = kp[(int64_t)key * a.k_l + 2 * p];
-        kx[i][1] = kp[(int64_t)key * a.k_l + 2 * p + 1];
+      if (krow[i] < rows) {
+        kx[i][0] = kt[koff[i]];
+        kx[i][1] = kt[koff[i] + 1];
         if constexpr (ROT) {
-          kc[i] = a.rc[(int64_t)key * (D / 2) + p];
-          ksn[i] = a.rs[(int64_t)key * (D / 2) + p];
+          kc[i] = a.rc[(int64_t)t * KT * (D / 2) + toff[i]];
+          ksn[i] = a.rs[(int64_t)t * KT * (D / 2) + toff[i]];
         }
       }
     }
 #pragma unroll
     for (int i = 0; i < VJOBS; ++i) {
-      const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
-      const int key = t * KT + r;
       f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-      vx[i] = key < L && e < KT * (D / 4) ? *(const f32x4_t*)(vp + (int64_t)key * a.v_l + 4 * c4) : z;
+      vx[i] = vrow[i] < rows ? *(const f32x4_t*)(vt + voff[i]) : z;
     }
   };
   auto store = [&](int buf) {
@@ -181,18 +197,22 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
         for (int u = 0; u < 4; ++u) st = mma_f32(kv[u], qf[4 * j4 + u], st);
       }
       const bool need_mask = (a.causal && key0 + 31 > q0_w) || key0 + 31 >= vlen || q0_w + 31 >= L;
-      float ts = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float p = rho8_exact(st[e] * scale);
-        if (need_mask) {
+      for (int e = 0; e < 16; ++e) st[e] = rho8_exact(st[e] * scale);
+      if (need_mask) {
+        // a side effect the compiler cannot move keeps this a branch on the wave-uniform test
+        // instead of a compare and a select per score in every tile
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
           const int key = key0 + 8 * (e >> 2) + 4 * g + (e & 3);
           const bool keep = key < vlen && qi < L && (!a.causal || key <= qi);
-          p = keep ? p : 0.f;
+          st[e] = keep ? st[e] : 0.f;
         }
-        st[e] = p;
-        ts += p;
       }
+      float ts = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ts += st[e];
       // two-level sums: the tile's own (row sum and PV from zero), then added to the running
       // ones, as the reference adds one block's dot(p, v) at a time
       // (src/kernels/pallas_afa.py:131-139); a single chain over L keys would carry a rounding
