@@ -207,11 +207,18 @@ FwdPlan fwd_plan(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, int64_t 
   if (dtype == AFA_F32 && afa::f32_fwd_supported((int)D) && f32_layout) {
     p.kind = FWD_F32;
     // fewer 128-query workgroups than CUs: split every query block's key tiles over up to
-    // 2 * CUs workgroups in all (partials in the workspace, then a combine kernel)
+    // 2 * CUs workgroups in all (partials in the workspace, then a combine kernel).  Fewer than
+    // the kernel's resident slots (4, 2 and 1 per CU at head_dim 32, 48-64 and 96-128) with rows
+    // of at least 1024 keys: split up to the slots.  Shorter rows do not repay the partials'
+    // traffic and the combine (a 16-shard ring hop of 256 keys: 31 against 39 us per hop).
     const int64_t nwg = B * H * ((L + 127) / 128);
     const int64_t key_tiles = (vlen + 31) / 32;
     const int64_t cus = cu_count();
-    if (nwg < cus && key_tiles > 1) p.nsplit = (int)std::min<int64_t>(key_tiles, (2 * cus + nwg - 1) / nwg);
+    const int64_t slots = cus * (D <= 32 ? 4 : D <= 64 ? 2 : 1);
+    if (nwg < cus && key_tiles > 1)
+      p.nsplit = (int)std::min<int64_t>(key_tiles, (2 * cus + nwg - 1) / nwg);
+    else if (nwg < slots && key_tiles >= 32)
+      p.nsplit = (int)std::min<int64_t>(key_tiles, (slots + nwg - 1) / nwg);
     if (p.nsplit > 1) p.total = align256((size_t)p.nsplit * B * H * L * (D + 1) * sizeof(float));
   }
   return p;
