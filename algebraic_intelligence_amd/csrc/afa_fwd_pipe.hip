@@ -157,13 +157,13 @@ template <int DP>
 using PipeTile = unsigned short[32 * DP];
 
 // Direct global -> LDS loads of key tile t (32 keys of K and of V) of one head into ring buffer
-// t % NB: slot s = tid + 256 i covers row s / CH, physical chunk s % CH; K chunk c of row r goes to
+// buf = t % NB: slot s = tid + 256 i covers row s / CH, physical chunk s % CH; K chunk c of row r goes to
 // c ^ (r mod CH) (every chunk position of the row in turn), V chunk c to v_swizzle; rows past L
 // read row L - 1 (finite data, masked keys).
 template <int D>
 __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padded_dim(D)>* lds_k,
                                                 PipeTile<padded_dim(D)>* lds_v, const unsigned short* kp,
-                                                const unsigned short* vp, int t) {
+                                                const unsigned short* vp, int t, int buf) {
   constexpr int DP = padded_dim(D);
   constexpr int KT = 32;
   constexpr int NB = PipeShape<DP>::NB;
@@ -172,8 +172,8 @@ __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padde
   constexpr int LPT = KT * CH / 256;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  unsigned short* kd = &lds_k[t % NB][0];
-  unsigned short* vd = &lds_v[t % NB][0];
+  unsigned short* kd = &lds_k[buf][0];
+  unsigned short* vd = &lds_v[buf][0];
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
     const int s = tid + 256 * i, r = s / CH, pc = s % CH;
@@ -226,16 +226,19 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
   const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
 
-  auto issue_tile = [&](int t) { pipe_issue_tile<D>(a, lds_k, lds_v, kp, vp, t); };
+  // tile t lives in ring buffer t % NB (t >= 0; NB is a power of two).  The callers pass the
+  // buffer: a constant in the loop over aligned groups of NB tiles, so that every LDS address
+  // there is a loop-invariant lane offset plus an immediate
+  auto issue_tile = [&](int t, int buf) { pipe_issue_tile<D>(a, lds_k, lds_v, kp, vp, t, buf); };
   u32x4_t kf[NK];
   u32x4_t vf[NDB][2];
-  auto read_kf = [&](int u) {
-    const unsigned short* base = &lds_k[u % NB][l32 * DP];
+  auto read_kf = [&](int buf) {
+    const unsigned short* base = &lds_k[buf][l32 * DP];
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & (CH - 1))) * 8));
   };
-  auto read_vf = [&](int u) {
-    const unsigned short* tile = lds_v[u % NB];
+  auto read_vf = [&](int buf) {
+    const unsigned short* tile = lds_v[buf];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -270,7 +273,7 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   __syncthreads();
   if (t_lo < t_hi) {
-    read_kf(t_lo);
+    read_kf(t_lo & (NB - 1));
 #pragma unroll
     for (int e = 0; e < 16; ++e) sA[e] = 0.f;
 #pragma unroll
@@ -281,7 +284,7 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   auto unit = [&](int u, f32x16_t& scur, f32x16_t& snxt) {
     if (u >= U) return;
     if (u + 1 < U) {
-      read_kf(u + 1);
+      read_kf((u + 1) & (NB - 1));
 #pragma unroll
       for (int e = 0; e < 16; ++e) snxt[e] = 0.f;
 #pragma unroll
@@ -318,7 +321,7 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
 #pragma unroll
       for (int e = 0; e < 4; ++e) pk[kk][e] = Elem<DT>::pack(p[kk * 8 + 2 * e], p[kk * 8 + 2 * e + 1]);
     __builtin_amdgcn_sched_barrier(0);
-    read_vf(u);
+    read_vf(u & (NB - 1));
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -327,14 +330,14 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   // The same unit where it is known to be one of the wave's units, to have a next one and to
   // need no mask: no branch and no select in its VALU stream (the guarded form's mask test is
   // if-converted into a compare and a select per score).
-  auto clean_unit = [&](int u, f32x16_t& scur, f32x16_t& snxt) {
-    read_kf(u + 1);
+  auto clean_unit = [&](int buf, f32x16_t& scur, f32x16_t& snxt) {  // buf = u % NB
+    read_kf((buf + 1) & (NB - 1));
 #pragma unroll
     for (int e = 0; e < 16; ++e) snxt[e] = 0.f;
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) snxt = mma16<DT>(kf[kc], qf[kc], snxt);
     // V(u)'s fragments are read here, so their LDS latency runs under the rho^8 chain
-    read_vf(u);
+    read_vf(buf);
     __builtin_amdgcn_sched_barrier(0);
     float p[16];
     if constexpr (FAST) {
@@ -365,11 +368,11 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
 
   // Step u: own loads of tile u+1 done (those of later tiles may remain), then publish them; the
   // barrier also ends every wave's unit u-1, the last reader of the buffer reused by the issue.
-  auto step = [&](int u) {
+  auto step = [&](int u, int buf) {  // buf = u % NB
     if (u + 2 < t_hi) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS * (NB - 3)));
     else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __syncthreads();
-    if (u + NB - 1 < t_hi) issue_tile(u + NB - 1);
+    if (u + NB - 1 < t_hi) issue_tile(u + NB - 1, (buf + NB - 1) & (NB - 1));
   };
   // Units are taken in pairs from the even t_lo, so S(u) sits in sA for even u and in sB for
   // odd u with no register copies.  Unit u is clean when u + 1 < U (a next unit exists) and no
@@ -383,17 +386,36 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   int uc = t_lo;
   while (uc < t_hi && clean(uc)) ++uc;
   int u = t_lo;
+  // clean units: one pair up to a multiple of NB, then groups of NB with constant buffers
+  static_assert(NB == 4, "the clean loop takes the ring's buffers in groups of four");
+  if ((u & (NB - 1)) != 0 && u + 1 < uc) {
+    step(u, u & (NB - 1));
+    clean_unit(u & (NB - 1), sA, sB);
+    step(u + 1, (u + 1) & (NB - 1));
+    clean_unit((u + 1) & (NB - 1), sB, sA);
+    u += 2;
+  }
+  for (; u + 3 < uc; u += 4) {
+    step(u, 0);
+    clean_unit(0, sA, sB);
+    step(u + 1, 1);
+    clean_unit(1, sB, sA);
+    step(u + 2, 2);
+    clean_unit(2, sA, sB);
+    step(u + 3, 3);
+    clean_unit(3, sB, sA);
+  }
   for (; u + 1 < uc; u += 2) {
-    step(u);
-    clean_unit(u, sA, sB);
-    step(u + 1);
-    clean_unit(u + 1, sB, sA);
+    step(u, u & (NB - 1));
+    clean_unit(u & (NB - 1), sA, sB);
+    step(u + 1, (u + 1) & (NB - 1));
+    clean_unit((u + 1) & (NB - 1), sB, sA);
   }
   for (; u < t_hi; u += 2) {
-    step(u);
+    step(u, u & (NB - 1));
     unit(u, sA, sB);
     if (u + 1 < t_hi) {
-      step(u + 1);
+      step(u + 1, (u + 1) & (NB - 1));
       unit(u + 1, sB, sA);
     }
   }
@@ -536,7 +558,8 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
     const int t_hi = min(pp.t1, ntiles), t_lo = min(pp.t0, t_hi);
     const unsigned short* kp = (const unsigned short*)a.k + b * a.k_b + h * a.k_h;
     const unsigned short* vp = (const unsigned short*)a.v + b * a.v_b + h * a.v_h;
-    for (int t = t_lo; t < t_lo + min(t_hi - t_lo, NB - 1); ++t) pipe_issue_tile<D>(a, lds_k, lds_v, kp, vp, t);
+    for (int t = t_lo; t < t_lo + min(t_hi - t_lo, NB - 1); ++t)
+      pipe_issue_tile<D>(a, lds_k, lds_v, kp, vp, t, t & (NB - 1));
   }
 
   // q fragments (B operand of S^T = K Q^T): query q0_w + l32, features kc*16 + 8g .. +7
