@@ -17,6 +17,8 @@
 // Small grids (fewer workgroups than CUs) split every query block's key tiles over blockIdx.y:
 // the numerator and denominator are sums over keys, so each split writes its partial O and row
 // sum, and afa_fwd_f32_combine_kernel adds them, adds the sink and divides.
+#include <climits>
+
 #include "afa_common.h"
 #include "afa_launch.h"
 
@@ -116,7 +118,7 @@ __global__ __launch_bounds__(256) void afa_fwd_f32_kernel(const FwdArgs a) {
 #pragma unroll
   for (int i = 0; i < VJOBS; ++i) {
     const int e = tid + 256 * i, r = e / (D / 4), c4 = e % (D / 4);
-    vrow[i] = e < KT * (D / 4) ? r : KT;  // past the tile: never loaded
+    vrow[i] = e < KT * (D / 4) ? r : INT_MAX;  // past the tile (head_dim 48): never loaded
     voff[i] = (int64_t)r * a.v_l + 4 * c4;
   }
   auto load = [&](int t) {
