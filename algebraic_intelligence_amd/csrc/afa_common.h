@@ -216,6 +216,31 @@ __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, cons
                : "memory", "m0");
 }
 
+// Buffer resource of a raw byte range [base, base + bytes) for the loads below: stride 0,
+// num_records = bytes, dword 3 selecting 32-bit data (gfx9 raw buffer access).  Every field is
+// made wave-uniform so the descriptor sits in scalar registers.
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+__device__ __forceinline__ i32x4_t raw_buffer_srd(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  i32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from the buffer at soff (uniform) + voff (per lane) into LDS at lds (the
+// wave's 1 KB destination, as above).  Lanes whose bytes lie past the buffer's range read zeros
+// instead of memory, so a tile that runs past the end of a head needs no clamp.
+__device__ __forceinline__ void lds_dma16_buf(i32x4_t srd, uint32_t soff, uint32_t voff, const void* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(srd), "s"(soff), "s"(m0)
+               : "memory", "m0");
+}
+
 // The same with a full 64-bit address per lane.
 __device__ __forceinline__ void lds_dma16(const void* src, const void* lds) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;

@@ -159,7 +159,8 @@ using PipeTile = unsigned short[32 * DP];
 // Direct global -> LDS loads of key tile t (32 keys of K and of V) of one head into ring buffer
 // buf = t % NB: slot s = tid + 256 i covers row s / CH, physical chunk s % CH; K chunk c of row r goes to
 // c ^ (r mod CH) (every chunk position of the row in turn), V chunk c to v_swizzle; rows past L
-// read row L - 1 (finite data, masked keys).
+// read zeros (buffer loads whose range ends with row L - 1) or, at head dims with padding
+// chunks, row L - 1: finite data for masked keys.
 template <int D>
 __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padded_dim(D)>* lds_k,
                                                 PipeTile<padded_dim(D)>* lds_v, const unsigned short* kp,
@@ -174,6 +175,22 @@ __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padde
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   unsigned short* kd = &lds_k[buf][0];
   unsigned short* vd = &lds_v[buf][0];
+  if constexpr (CHD == CH) {
+    // buffer loads: the head's rows [0, L) are the buffer, so rows past L read zeros (finite,
+    // masked keys); the tile is a uniform offset and each lane's offset is the same in every tile
+    const i32x4_t ksrd = raw_buffer_srd(kp, (uint32_t)((a.L - 1) * (int)a.k_l + D) * 2u);
+    const i32x4_t vsrd = raw_buffer_srd(vp, (uint32_t)((a.L - 1) * (int)a.v_l + D) * 2u);
+    const uint32_t ks0 = __builtin_amdgcn_readfirstlane((uint32_t)(t * KT * (int)a.k_l) * 2u);
+    const uint32_t vs0 = __builtin_amdgcn_readfirstlane((uint32_t)(t * KT * (int)a.v_l) * 2u);
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int s = tid + 256 * i, r = s / CH, pc = s % CH;
+      const int lk = pc ^ (r & (CH - 1)), lv = v_swizzle<DP>(r, pc);
+      lds_dma16_buf(ksrd, ks0, (uint32_t)(r * (int)a.k_l + lk * 8) * 2u, kd + (256 * i + wave * 64) * 8);
+      lds_dma16_buf(vsrd, vs0, (uint32_t)(r * (int)a.v_l + lv * 8) * 2u, vd + (256 * i + wave * 64) * 8);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
     const int s = tid + 256 * i, r = s / CH, pc = s % CH;
