@@ -294,19 +294,20 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
     // analysis loses track of it inside the rho^8-form branch
     const int t = __builtin_amdgcn_readfirstlane(tile_index);
     if constexpr (D == DP) {
-      // buffer loads over the head's L rows: rows past L read zeros (finite, masked keys), the
-      // tile is a uniform offset and each lane's offset is the same in every tile
-      const i32x4_t ksrd = raw_buffer_srd(kp, (uint32_t)(L * D) * 2u);
-      const i32x4_t vsrd = raw_buffer_srd(vp, (uint32_t)(L * D) * 2u);
+      // buffer loads: each resource runs from the tile's first row to the end of the head's L
+      // rows, so rows past L read zeros (finite, masked keys) and nothing past the head is read;
+      // each lane's offset is the same in every tile
       const uint32_t s0 = (uint32_t)(t * KT * D) * 2u;
+      const i32x4_t ksrd = raw_buffer_srd_at(kp, (uint32_t)(L * D) * 2u, s0);
+      const i32x4_t vsrd = raw_buffer_srd_at(vp, (uint32_t)(L * D) * 2u, s0);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int c = tid + 256 * i;
         const int row = c / NCK, pc = c % NCK;
         const int lc = pc ^ swz_key<DP>(row);
         const uint32_t off = (uint32_t)(row * D + lc * 8) * 2u;
-        lds_dma16_buf(ksrd, s0, off, &lds_k[t & 1][(256 * i + wave * 64) * 8]);
-        lds_dma16_buf(vsrd, s0, off, &lds_v[t & 1][(256 * i + wave * 64) * 8]);
+        lds_dma16_buf(ksrd, off, &lds_k[t & 1][(256 * i + wave * 64) * 8]);
+        lds_dma16_buf(vsrd, off, &lds_v[t & 1][(256 * i + wave * 64) * 8]);
       }
       return;
     }
@@ -507,18 +508,19 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
 
   auto issue = [&](int t) {
     if constexpr (D == DP) {
-      // buffer loads over the head's L rows (rows past L read zeros), as in the dQ kernel
-      const i32x4_t qsrd = raw_buffer_srd(qp, (uint32_t)(L * D) * 2u);
-      const i32x4_t gsrd = raw_buffer_srd(gp, (uint32_t)(L * D) * 2u);
+      // buffer loads from the tile's first row to the end of the head's L rows (rows past L
+      // read zeros), as in the dQ kernel
       const uint32_t s0 = __builtin_amdgcn_readfirstlane((uint32_t)(t * QT * D) * 2u);
+      const i32x4_t qsrd = raw_buffer_srd_at(qp, (uint32_t)(L * D) * 2u, s0);
+      const i32x4_t gsrd = raw_buffer_srd_at(gp, (uint32_t)(L * D) * 2u, s0);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int c = tid + 256 * i;
         const int row = c / NCK, pc = c % NCK;
         const int lc = pc ^ swz_key<DP>(row);
         const uint32_t off = (uint32_t)(row * D + lc * 8) * 2u;
-        lds_dma16_buf(qsrd, s0, off, &lds_q[t & 1][(256 * i + wave * 64) * 8]);
-        lds_dma16_buf(gsrd, s0, off, &lds_g[t & 1][(256 * i + wave * 64) * 8]);
+        lds_dma16_buf(qsrd, off, &lds_q[t & 1][(256 * i + wave * 64) * 8]);
+        lds_dma16_buf(gsrd, off, &lds_g[t & 1][(256 * i + wave * 64) * 8]);
       }
     } else {
 #pragma unroll

@@ -230,14 +230,25 @@ __device__ __forceinline__ i32x4_t raw_buffer_srd(const void* base, uint32_t byt
   return r;
 }
 
-// 16 bytes per lane from the buffer at soff (uniform) + voff (per lane) into LDS at lds (the
-// wave's 1 KB destination, as above).  Lanes whose bytes lie past the buffer's range read zeros
-// instead of memory, so a tile that runs past the end of a head needs no clamp.
-__device__ __forceinline__ void lds_dma16_buf(i32x4_t srd, uint32_t soff, uint32_t voff, const void* lds) {
+// Buffer resource over the byte range [base + off, base + bytes), empty when off >= bytes.  A
+// tile's offset goes into the resource's base, never into the instruction's scalar offset: the
+// range check of a raw buffer access covers the lane offset and the instruction offset only, and
+// the scalar offset is added to the address after the check.  Only a range that starts at the
+// tile makes the bytes past `bytes` read as zeros.
+__device__ __forceinline__ i32x4_t raw_buffer_srd_at(const void* base, uint32_t bytes, uint32_t off) {
+  return raw_buffer_srd((const char*)base + off, bytes > off ? bytes - off : 0u);
+}
+
+// 16 bytes per lane from the buffer at voff (per lane) into LDS at lds (the wave's 1 KB
+// destination, as above); the scalar offset is 0.  Lanes whose 16 bytes start at or past the
+// buffer's range read zeros instead of memory (the range check of a raw buffer), so a tile whose
+// resource starts at the tile (raw_buffer_srd_at) and ends with the head's last row needs no
+// clamp for the rows past the end of the head.
+__device__ __forceinline__ void lds_dma16_buf(i32x4_t srd, uint32_t voff, const void* lds) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
-  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "v"(voff), "s"(srd), "s"(soff), "s"(m0)
+               : "v"(voff), "s"(srd), "s"(m0)
                : "memory", "m0");
 }
 

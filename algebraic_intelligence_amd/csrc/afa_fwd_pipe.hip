@@ -176,18 +176,19 @@ __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padde
   unsigned short* kd = &lds_k[buf][0];
   unsigned short* vd = &lds_v[buf][0];
   if constexpr (CHD == CH) {
-    // buffer loads: the head's rows [0, L) are the buffer, so rows past L read zeros (finite,
-    // masked keys); the tile is a uniform offset and each lane's offset is the same in every tile
-    const i32x4_t ksrd = raw_buffer_srd(kp, (uint32_t)((a.L - 1) * (int)a.k_l + D) * 2u);
-    const i32x4_t vsrd = raw_buffer_srd(vp, (uint32_t)((a.L - 1) * (int)a.v_l + D) * 2u);
+    // buffer loads: each resource runs from the tile's first row to the end of the head's row
+    // L - 1, so rows past L read zeros (finite, masked keys) and nothing past the head is read;
+    // each lane's offset is the same in every tile
     const uint32_t ks0 = __builtin_amdgcn_readfirstlane((uint32_t)(t * KT * (int)a.k_l) * 2u);
     const uint32_t vs0 = __builtin_amdgcn_readfirstlane((uint32_t)(t * KT * (int)a.v_l) * 2u);
+    const i32x4_t ksrd = raw_buffer_srd_at(kp, (uint32_t)((a.L - 1) * (int)a.k_l + D) * 2u, ks0);
+    const i32x4_t vsrd = raw_buffer_srd_at(vp, (uint32_t)((a.L - 1) * (int)a.v_l + D) * 2u, vs0);
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int s = tid + 256 * i, r = s / CH, pc = s % CH;
       const int lk = pc ^ (r & (CH - 1)), lv = v_swizzle<DP>(r, pc);
-      lds_dma16_buf(ksrd, ks0, (uint32_t)(r * (int)a.k_l + lk * 8) * 2u, kd + (256 * i + wave * 64) * 8);
-      lds_dma16_buf(vsrd, vs0, (uint32_t)(r * (int)a.v_l + lv * 8) * 2u, vd + (256 * i + wave * 64) * 8);
+      lds_dma16_buf(ksrd, (uint32_t)(r * (int)a.k_l + lk * 8) * 2u, kd + (256 * i + wave * 64) * 8);
+      lds_dma16_buf(vsrd, (uint32_t)(r * (int)a.v_l + lv * 8) * 2u, vd + (256 * i + wave * 64) * 8);
     }
     return;
   }
@@ -444,6 +445,21 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   // the point where every XCD sees them), so no cache-wide write-back or invalidate is needed:
   // a part's stores are complete (vmcnt 0) before its count, and the last part reads after its
   // own count.
+  //
+  // This hand-off has no release/acquire edge in the HIP memory model; it is correct because of
+  // how gfx950 executes these instructions, and the bitwise-repeatability test of the key split
+  // guards it:
+  //  * an agent-scope relaxed store is a global store with the sc1 bit, written through the
+  //    XCD's L2 to memory-side coherent storage, and vmcnt counts it complete only once that
+  //    write is acknowledged, so every part's partials are visible device-wide before its
+  //    s_waitcnt vmcnt(0) ends and the barrier lets tid 0 issue the counter atomic;
+  //  * the counter atomic executes at device scope, and the last part's partial loads are issued
+  //    only after it returns (its value decides the branch);
+  //  * an agent-scope relaxed load carries sc1 as well and misses the non-coherent cache levels,
+  //    so it returns the value written through, not a stale line of this XCD's L2.
+  // A target whose stores are acknowledged before they are device-visible, or whose sc1 loads
+  // may hit stale lines, would need an acq_rel fetch_add by tid 0 (a whole-L2 write-back and
+  // invalidate on gfx950, which made the split 2-4x slower).
   if (pp.nparts > 1) {
     __shared__ int ks_last;
     // a part's partial, lane-major so that every store and load instruction covers 256
