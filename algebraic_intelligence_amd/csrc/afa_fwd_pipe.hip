@@ -648,10 +648,13 @@ PipeSplit pipe_split_plan(int head_dim, int64_t BH, int64_t L, bool causal, int 
   for (int64_t q = 0; q < nqb; ++q) total += tiles(q);
   total *= BH;
   // parts of about the balanced load per workgroup slot, at least 16 tiles (512 keys) each, and
-  // the partials (fp32 rows of every part of every split block) within 48 MiB
+  // the partials (fp32 rows of every part of every split block) within 48 MiB.  No split when the
+  // longest block is within 50% of a part: storing and adding the partials then costs more than
+  // the shorter critical path saves (B=32 H=4 L=1024 D=64 causal, whose longest block is 1.33
+  // parts: 334 TFLOP/s split, 353 unsplit; B=4 H=8 L=2048, 2.67 parts: 386 split, 371 unsplit)
   for (int64_t T = std::max<int64_t>((total + slots - 1) / slots, 16); T <= tiles(nqb - 1); T *= 2) {
     T = (T + 1) & ~(int64_t)1;
-    if (tiles(nqb - 1) * 4 <= T * 5) return ps;  // the longest block is within 25% of a part
+    if (tiles(nqb - 1) * 2 <= T * 3) return ps;
     int64_t q0 = 0;
     while (tiles(q0) <= T) ++q0;
     const int64_t pmax = (tiles(nqb - 1) + T - 1) / T;

@@ -141,6 +141,20 @@ def test_afa_fwd_workspace_contract(lib):
     assert lib.afa_fwd_workspace_size(_lib.AFA_F64, 1, 1, 64, 64, 0) == 0
 
 
+def test_key_split_plan(lib):
+    """The 128-query kernel splits a query block's keys over several workgroups only when its
+    longest block exceeds the balanced load per workgroup slot by more than half (planned for a
+    256-CU MI355X, the CU count the library assumes without a device): B=4 H=8 L=2048 (longest
+    block 2.67 parts) splits, B=32 H=4 L=1024 (1.33 parts, faster unsplit) does not, so its
+    workspace holds only the key bounds and the rotated k."""
+    def base(B, H, L, D, rot):
+        n = -(-B * H * -(-L // 64) * 4 // 256) * 256
+        return n + (-(-B * H * L * D * 2 // 256) * 256 if rot else 0)
+
+    assert lib.afa_fwd_workspace_size(_lib.AFA_BF16, 32, 4, 1024, 64, 1) == base(32, 4, 1024, 64, True)
+    assert lib.afa_fwd_workspace_size(_lib.AFA_BF16, 4, 8, 2048, 64, 0) > base(4, 8, 2048, 64, False)
+
+
 def test_afa_bwd_workspace_contract(lib):
     plain = lib.afa_bwd_workspace_size(_lib.AFA_BF16, 2, 16, 8192, 128, 0)
     rot = lib.afa_bwd_workspace_size(_lib.AFA_BF16, 2, 16, 8192, 128, 1)
