@@ -170,8 +170,11 @@ def exact_afa_reference(q, k, v, sink_omega: float = 0.5, causal: bool = False) 
     """Untiled reference contract (src/kernels/pallas_afa.py:267-297): q * scale rounded to
     q.dtype before the dot, row sum of P cast to v.dtype, out = O * (1 / (D + sink)).
 
-    For bf16/fp16 inputs the reference additionally evaluates S and rho^8 in the input dtype;
-    here they are evaluated in fp32.
+    For bf16/fp16 inputs every op is rounded to the input dtype as the reference's JAX program
+    types it: the scale itself, the scores, each step of rho^8, the P V product, the row sum,
+    D + sink, its reciprocal and the product.  The summation orders, which the program leaves
+    to XLA, are fixed by the kernel (8 fma chains per score added pairwise, key order for the
+    P V product and the row sum).
     """
     return exact_afa_with_denominator(q, k, v, sink_omega, causal)[0]
 

@@ -8,8 +8,10 @@
 //
 // Forward contract: src/kernels/pallas_afa.py:104-151 (S in the accumulation type, rho(S)^8,
 // masks, P cast to v.dtype for PV, unrounded row sum, out = O / (D + Omega)); with
-// AFA_FLAG_EXACT_REF the exact_afa_reference contract (:283-297): q * scale rounded to q.dtype
-// before the dot, row sum of the cast P, out = O * (1 / (D + Omega)).
+// AFA_FLAG_EXACT_REF the exact_afa_reference contract (:267-327): q * scale rounded to q.dtype
+// before the dot, row sum of the cast P, out = O * (1 / (D + Omega)); for bf16 / fp16 inputs
+// every op of that program is rounded to the input dtype as its JAX typing does (the score, each
+// step of rho^8, the P V product, the row sum, D + Omega, its reciprocal and the product).
 // Backward contract: src/kernels/pallas_afa.py:437-522 (E = rowsum(g * out); w = rho^8 / d;
 // ds = 8 scale r w (g.v - E); matmul operands cast to the input dtype, accumulation in the
 // accumulation type).
@@ -73,6 +75,24 @@ __device__ __forceinline__ T group8_sum(T x) {
   x += __shfl_xor(x, 2);
   x += __shfl_xor(x, 4);
   return x;
+}
+
+// rho(s)^8 of exact_afa_reference for bf16 / fp16 inputs (src/kernels/pallas_afa.py:32-49 on the
+// scores of :284, which are bf16 / fp16): each elementwise op of _vmu_octic_kernel is evaluated in
+// fp32 and rounded to the input dtype, as every jnp op on such an array returns that dtype; rsqrt
+// is 1 / sqrt, each rounded in fp32.
+template <int DT>
+__device__ __forceinline__ float rho8_stepwise(float s) {
+#pragma clang fp contract(off)
+  const float s_sq = Elem<DT>::round(s * s);
+  const float rad = Elem<DT>::round(1.0f + s_sq);
+  const float r = Elem<DT>::round(1.0f / __builtin_sqrtf(rad));
+  const float u = Elem<DT>::round(s * r);
+  const float rho = s < 0.0f ? Elem<DT>::round(r / Elem<DT>::round(1.0f - u))
+                             : Elem<DT>::round(s + Elem<DT>::round(rad * r));
+  const float k2 = Elem<DT>::round(rho * rho);
+  const float k4 = Elem<DT>::round(k2 * k2);
+  return Elem<DT>::round(k4 * k4);
 }
 
 // Cayley rotation of one (even, odd) pair; products and sums rounded separately.
@@ -139,6 +159,11 @@ __global__ __launch_bounds__(256) void afa_fwd_generic_kernel(const GenArgs a) {
   typedef typename Acc<DT>::T T;
   constexpr int M = DMAX / 8;
   constexpr int KTG = gen_tile_rows<DT, DMAX>();
+  // bf16 / fp16 under AFA_FLAG_EXACT_REF: every op of exact_afa_reference rounded to the input
+  // dtype, in a fixed order (the score as 8 fma chains over features sub + 8m added by the xor
+  // butterfly, the P V product as an fma chain and the row sum as a sum in key order)
+  constexpr bool HALF = DT == AFA_BF16 || DT == AFA_F16;
+  const bool step = HALF && a.exact_ref;
   __shared__ T ks[KTG][DMAX];
   __shared__ T vs[KTG][DMAX];
 
@@ -182,8 +207,10 @@ __global__ __launch_bounds__(256) void afa_fwd_generic_kernel(const GenArgs a) {
       }
     }
     if (a.exact_ref) {
+      // q * scale rounded to q's dtype; the reference's Python float scale takes q's dtype first
+      const T sc = HALF ? rnd<DT>(scale) : scale;
 #pragma unroll
-      for (int m = 0; m < M; ++m) qv[m] = rnd<DT>(qv[m] * scale);
+      for (int m = 0; m < M; ++m) qv[m] = rnd<DT>(qv[m] * sc);
     }
   }
 
@@ -199,17 +226,33 @@ __global__ __launch_bounds__(256) void afa_fwd_generic_kernel(const GenArgs a) {
     for (int jj = 0; jj < nk; ++jj) {
       const int j = k0 + jj;
       T part = 0;
+      if (step) {
 #pragma unroll
-      for (int m = 0; m < M; ++m)
-        if (sub + 8 * m < D) part += qv[m] * ks[jj][sub + 8 * m];
+        for (int m = 0; m < M; ++m)
+          if (sub + 8 * m < D) part = __builtin_fmaf(qv[m], ks[jj][sub + 8 * m], part);
+      } else {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          if (sub + 8 * m < D) part += qv[m] * ks[jj][sub + 8 * m];
+      }
       const T sdot = group8_sum(part);
-      const T s = a.exact_ref ? sdot : sdot * scale;
-      T p = rho8_acc(s);
+      T p;
+      if constexpr (HALF) {
+        p = step ? rho8_stepwise<DT>(rnd<DT>(sdot)) : rho8_acc(a.exact_ref ? sdot : sdot * scale);
+      } else {
+        p = rho8_acc(a.exact_ref ? sdot : sdot * scale);
+      }
       if (a.causal && j > qi) p = 0;
       const T pv = rnd<DT>(p);
+      if (step) {
 #pragma unroll
-      for (int m = 0; m < M; ++m)
-        if (sub + 8 * m < D) o[m] += pv * vs[jj][sub + 8 * m];
+        for (int m = 0; m < M; ++m)
+          if (sub + 8 * m < D) o[m] = __builtin_fmaf(pv, vs[jj][sub + 8 * m], o[m]);
+      } else {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          if (sub + 8 * m < D) o[m] += pv * vs[jj][sub + 8 * m];
+      }
       dsum += a.exact_ref ? pv : p;
     }
   }
@@ -221,13 +264,14 @@ __global__ __launch_bounds__(256) void afa_fwd_generic_kernel(const GenArgs a) {
       if (sub + 8 * m < D) acc_row((T*)a.out + obase + sub + 8 * m, o[m], a.acc);
     if (sub == 0) acc_row((T*)a.denom + (int64_t)bh * a.L + qi, dsum, a.acc);
   } else if (qi < a.L) {
-    const T tot = dsum + (T)a.omega;
+    // under step, the row sum, Omega and their sum are each rounded to the input dtype
+    const T tot = step ? rnd<DT>(rnd<DT>(dsum) + rnd<DT>((T)a.omega)) : dsum + (T)a.omega;
     const int64_t obase = b * a.o_b + h * a.o_h + (int64_t)qi * a.o_l;
     if (a.exact_ref) {
       const T inv = rnd<DT>(T(1) / tot);
 #pragma unroll
       for (int m = 0; m < M; ++m)
-        if (sub + 8 * m < D) st<DT>(a.out, obase + sub + 8 * m, o[m] * inv);
+        if (sub + 8 * m < D) st<DT>(a.out, obase + sub + 8 * m, (step ? rnd<DT>(o[m]) : o[m]) * inv);
     } else {
 #pragma unroll
       for (int m = 0; m < M; ++m)

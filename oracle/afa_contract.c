@@ -406,6 +406,74 @@ int oracle_afa_bwd(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, const 
 }
 
 /* Elementwise helpers exposed for the checker tests. */
+/* ---------------------------------------------------------------- exact_afa_reference */
+/* The untiled reference of src/kernels/pallas_afa.py:267-327 for bf16 / fp16 inputs, as its JAX
+ * program types every value: each jnp op on a bf16 (fp16) array returns bf16 (fp16), so each
+ * result below is evaluated in fp32 and rounded to the input dtype:
+ *   q_scaled = (q * scale).astype(q.dtype), the Python float scale taking q's dtype (:281-283);
+ *   s = q_scaled @ k^T, accumulated in fp32 and rounded                          (:284);
+ *   p = _vmu_octic_kernel(s), every elementwise op rounded                     (:32-49, :286);
+ *   causal mask; p_v = p.astype(v.dtype) (already v's dtype)                     (:288-292);
+ *   o = p_v @ v (fp32 accumulation, rounded); d = sum(p_v) (jnp.sum accumulates bf16 and fp16
+ *   in fp32, then rounds)                                                        (:293-294);
+ *   d_total = d + Omega; inv = reciprocal(d_total); out = o * inv, each rounded  (:296-297, :320-323).
+ * XLA may keep some of these intermediates in fp32 (its excess-precision option) and sums in its
+ * own order; neither is fixed by the program, so this restatement fixes them: the dot product
+ * of a score is 8 fma chains over features d = sub + 8m (sub = 0..7, m ascending) added as
+ * ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), the products p_v v and the sums over keys run
+ * as fma / add chains in key order.  rsqrt is 1 / sqrt, each rounded in fp32 (lax.rsqrt's
+ * rounding on XLA-CPU is not fixed either). */
+static inline float rho8_step(float s, int dt) {
+  const float s_sq = round_to(s * s, dt);
+  const float rad = round_to(1.0f + s_sq, dt);
+  const float r = round_to(1.0f / sqrtf(rad), dt);
+  const float u = round_to(s * r, dt);
+  const float rho = s < 0.0f ? round_to(r / round_to(1.0f - u, dt), dt) : round_to(s + round_to(rad * r, dt), dt);
+  const float k2 = round_to(rho * rho, dt);
+  const float k4 = round_to(k2 * k2, dt);
+  return round_to(k4 * k4, dt);
+}
+
+int oracle_afa_exact_ref(int dtype, int64_t B, int64_t H, int64_t L, int64_t D, const void* q, const void* k,
+                         const void* v, void* out, float* d_out, double sink_omega, int causal, int nthreads) {
+  if (dtype != DT_BF16 && dtype != DT_F16) return 4;
+  if (B <= 0 || H <= 0 || L <= 0 || D <= 0) return 1;
+  const float scale = round_to((float)(1.0 / sqrt((double)D)), dtype);
+  const float omega = round_to((float)sink_omega, dtype);
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads_for(nthreads))
+  for (int64_t task = 0; task < B * H * L; ++task) {
+    const int64_t bh = task / L, row = task % L;
+    const int64_t base = bh * L * D;
+    float* qs = malloc(sizeof(float) * D);
+    float* o = calloc(D, sizeof(float));
+    for (int64_t d = 0; d < D; ++d) qs[d] = round_to(load_in(q, base + row * D + d, dtype) * scale, dtype);
+    float dsum = 0.0f;
+    const int64_t jend = causal ? row + 1 : L;
+    for (int64_t j = 0; j < jend; ++j) {
+      float c[8];
+      for (int sub = 0; sub < 8; ++sub) {
+        c[sub] = 0.0f;
+        for (int64_t d = sub; d < D; d += 8) c[sub] = fmaf(qs[d], load_in(k, base + j * D + d, dtype), c[sub]);
+      }
+      const float sdot = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+      const float p = rho8_step(round_to(sdot, dtype), dtype);
+      for (int64_t d = 0; d < D; ++d) o[d] = fmaf(p, load_in(v, base + j * D + d, dtype), o[d]);
+      dsum += p;
+    }
+    const float tot = round_to(round_to(dsum, dtype) + omega, dtype);
+    const float inv = round_to(1.0f / tot, dtype);
+    for (int64_t d = 0; d < D; ++d) store_out(out, base + row * D + d, round_to(o[d], dtype) * inv, dtype);
+    if (d_out) d_out[bh * L + row] = tot;
+    free(qs);
+    free(o);
+  }
+  return 0;
+}
+
+void oracle_rho8_step(const float* x, float* y, int64_t n, int dtype) {
+  for (int64_t i = 0; i < n; ++i) y[i] = rho8_step(x[i], dtype);
+}
+
 void oracle_rho8_f32(const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = rho8_f32(x[i]);
 }

@@ -34,6 +34,9 @@ def lib():
                                      ci, i64, ci]
         L.oracle_afa_bwd.restype = ci
         L.oracle_rho8_f32.argtypes = [vp, vp, i64]
+        L.oracle_afa_exact_ref.argtypes = [ci, i64, i64, i64, i64, vp, vp, vp, vp, vp, dbl, ci, ci]
+        L.oracle_afa_exact_ref.restype = ci
+        L.oracle_rho8_step.argtypes = [vp, vp, i64, ci]
         L.oracle_bf16_round.argtypes = [vp, vp, i64]
         L.oracle_f16_round.argtypes = [vp, vp, i64]
         L.oracle_max_threads.restype = ci
@@ -110,6 +113,30 @@ def afa_fwd(q, k, v, dtype, sink_omega=0.5, causal=False, valid_len=None, rotary
     if rc_code:
         raise ValueError(f"oracle_afa_fwd rejected the arguments (code {rc_code})")
     return out, dd
+
+
+def afa_exact_ref(q, k, v, dtype, sink_omega=0.5, causal=False, nthreads=0):
+    """exact_afa_with_denominator (src/kernels/pallas_afa.py:300-327) for bf16 / fp16 bit patterns,
+    every op rounded to the input dtype as the reference's JAX program types it.  Returns
+    (out bits, d_total as float32 holding values of the input dtype) with d_total (B, H, L, 1)."""
+    q, k, v = _c(q, dtype), _c(k, dtype), _c(v, dtype)
+    B, H, L, D = q.shape
+    out = np.empty_like(q)
+    dd = np.empty((B, H, L, 1), dtype=np.float32)
+    rc = lib().oracle_afa_exact_ref(dtype, B, H, L, D, _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dd),
+                                    float(sink_omega), int(bool(causal)), nthreads)
+    if rc:
+        raise ValueError(f"oracle_afa_exact_ref rejected the arguments (code {rc})")
+    return out, dd
+
+
+def rho8_step(x, dtype):
+    """rho(s)^8 of the reference's _vmu_octic_kernel with every op rounded to bf16 / fp16
+    (x: float32 values of that dtype)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().oracle_rho8_step(_ptr(x), _ptr(y), x.size, dtype)
+    return y
 
 
 def afa_bwd(q, k, v, out, d_total, g, dtype, causal=False, valid_len=None, nthreads=0):

@@ -282,6 +282,41 @@ def test_exact_afa_reference(dtype):
     assert normwise(to_f64(A.exact_afa_reference(q, k, v, 0.5, True)), ref) <= tol
 
 
+@pytest.mark.parametrize("shape", [(1, 2, 96, 64), (2, 3, 200, 128), (1, 2, 333, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype,scale", [(torch.bfloat16, 1.0), (torch.float16, 0.3)])
+def test_exact_afa_reference_half(dtype, scale, causal, shape):
+    """exact_afa_reference / exact_afa_with_denominator in bf16 and fp16 (pallas_afa.py:267-327):
+    every op of the reference program rounded to the input dtype.  Bit for bit equal to the C
+    oracle's restatement (which fixes the summation orders the program leaves open), within the
+    reference's bf16 parity gate of float64 (4e-2; fp16 1e-2, on inputs scaled so rho^8 stays below
+    fp16's maximum, past which the reference's fp16 formula overflows), and the distance to the
+    fp32-internal contract of pallas_afa_forward reported."""
+    B, H, L, D = shape
+    q, k, v = make_qkv(shape, dtype, seed=72 + D + causal, scale=scale)
+    out, den = A.exact_afa_with_denominator(q, k, v, 0.5, causal)
+    assert den.dtype == dtype and den.shape == (B, H, L, 1)
+    code = C.DT_BF16 if dtype == torch.bfloat16 else C.DT_F16
+    c_out, c_den = C.afa_exact_ref(to_bits(q), to_bits(k), to_bits(v), code, 0.5, causal)
+    assert np.array_equal(to_bits(out), c_out)
+    assert np.array_equal(den.float().cpu().numpy(), c_den)
+    assert torch.equal(A.exact_afa_reference(q, k, v, 0.5, causal), out)
+    ref, rden = O.afa_forward(to_f64(q), to_f64(k), to_f64(v), 0.5, causal, return_denominator=True)
+    f3, _ = A.pallas_afa_forward(q, k, v, 0.5, causal, block_q=L, block_k=L, return_denominator=True)
+    e64, e_d, e_f3 = normwise(to_f64(out), ref), normwise(to_f64(den), rden), normwise(to_f64(out), to_f64(f3))
+    print(f"{dtype} {shape} causal={causal}: vs float64 {e64:.2e} (d_total {e_d:.2e}); "
+          f"vs the fp32-internal forward {e_f3:.2e}")
+    # how far the reference's own formula is from float64: a weight rounded op by op carries up
+    # to about 39 units of the dtype's half-ulp (8 from the score's rounding through
+    # d rho^8 / rho^8 = 8 ds / sqrt(1 + s^2), rho's ~3 roundings multiplied by 8 through the three
+    # squarings, and 7 from the squarings themselves): 7.6% in bf16, 1.9% in fp16.  A causal row
+    # with few keys has its d_total set by one or two weights (measured up to 4.1e-2 in bf16); the
+    # output, a ratio of sums of the same rounded weights, stays within the reference's bf16
+    # parity gate (4e-2; measured up to 2.8e-2)
+    assert e64 <= (4e-2 if dtype == torch.bfloat16 else 1e-2)
+    assert e_d <= (8e-2 if dtype == torch.bfloat16 else 2e-2)
+
+
 # ------------------------------------------------------------------------------ A-Softmax / octic
 @pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-13), (torch.float32, 2e-5), (torch.bfloat16, 1.6e-2)])
 @pytest.mark.parametrize("n", [1, 3, 7, 64])
