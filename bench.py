@@ -8,7 +8,8 @@ c3, is the metric's own configuration): c2 (B=4 H=8 L=2048 D=64 bf16 causal), c4
 D=128 bf16 causal forward) and c5bwd (its analytical backward, 10 B H D N_pairs FLOPs); ring16,
 c5ring8 and c3ring8 time distributed_ring_afa with its shards' hops run in turn on this GPU;
 c3hop8 and c5hop8 time one ring hop at one GPU's shard shape, c3share8 C3's per-GPU share under
-8-way batch x heads sharding.
+8-way batch x heads sharding; flash_c3, flash_tpu2k and flash_tpu4k time this library's forward
+beside torch's softmax FlashAttention at the same shapes (the reference's own comparison).
 
 Workload (C3): B=8, H=12, L=4096, D=64, bf16, causal, q/k Cayley-rotated in-kernel with
 Cayley parameters t_i = 10000^(-2i/D); q, k, v ~ N(0, 1) synthetic, resident in HBM.
@@ -99,6 +100,71 @@ def warm_up(step, args):
     return n, round(time.perf_counter() - t0, 3)
 
 
+def power_sample(step, seconds=1.5):
+    """Run `step` back to back for `seconds` while sampling the board with amd-smi: the socket
+    power (W) and the current clock of each XCD's graphics domain (MHz), as medians over the
+    samples.  MI355X's board power limit is 1400 W; a workload drawing that much runs below the
+    2.4 GHz maximum clock, and the dense MFMA peak assumes the maximum."""
+    import re
+    import shutil
+    import subprocess
+    import threading
+
+    import torch
+
+    exe = shutil.which("amd-smi")
+    if exe is None:
+        return {"available": False, "reason": "amd-smi not found"}
+    texts = []
+    stop = threading.Event()
+
+    def sampler():
+        time.sleep(0.4)
+        while not stop.is_set():
+            try:
+                r = subprocess.run([exe, "metric", "-g", "0", "--power", "--clock"], capture_output=True,
+                                   text=True, timeout=10)
+                texts.append(r.stdout)
+            except (OSError, subprocess.SubprocessError):
+                return
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds or (not texts and time.perf_counter() - t0 < 4 * seconds):
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=15)
+    power, clocks = [], []
+    for text in texts:
+        section, per = None, []
+        for raw in text.splitlines():
+            line = raw.strip()
+            m = re.match(r"SOCKET_POWER:\s*([0-9.]+)\s*W", line)
+            if m:
+                power.append(float(m.group(1)))
+            m = re.match(r"(GFX_\d+|MEM_\d+|[A-Z_]+\d*):$", line)
+            if m:
+                section = m.group(1)
+            m = re.match(r"CLK:\s*([0-9.]+)\s*MHz", line)
+            if m and section is not None and section.startswith("GFX_"):
+                per.append(float(m.group(1)))
+        if per:
+            clocks.append(per)
+    if not power:
+        return {"available": False, "reason": "no SOCKET_POWER in amd-smi output"}
+    import numpy as np
+
+    out = {"available": True, "samples": len(power), "socket_w": float(np.median(power)), "limit_w": 1400.0}
+    if clocks:
+        c = np.median(np.array(clocks), axis=0)
+        out.update({"gfx_mhz_per_xcd": [round(float(x)) for x in c], "gfx_mhz_mean": round(float(c.mean())),
+                    "gfx_mhz_max": 2400})
+    return out
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,10 +174,11 @@ def parse():
                     help="keep running untimed warmup steps until this much time has passed (the GPU "
                          "raises its clock over the first tens of milliseconds of load)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-power", action="store_true", help="skip the board power / clock sample")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--workload", default="c3",
                     choices=sorted(WORKLOADS) + sorted(SOFTMAX_WORKLOADS) + sorted(OACE_WORKLOADS)
-                    + sorted(RING_WORKLOADS) + sorted(HOP_WORKLOADS))
+                    + sorted(RING_WORKLOADS) + sorted(HOP_WORKLOADS) + sorted(FLASH_WORKLOADS))
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run a plain device copy of MIB MiB --steps times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -431,6 +498,84 @@ def ring_bench(args, dev):
     }), flush=True)
 
 
+# AFA against softmax FlashAttention on the same GPU, the reference's own bar for this path
+# (scripts/run_phase6_tpu.py:147-240: pallas_afa_forward against JAX's Pallas flash attention on
+# the same q, k, v; PASS at a throughput ratio >= 0.85; results/phase6/tpu/metrics.json:294-300
+# gives 0.9841 at L=2048 and 0.9967 at L=4096).  name -> (B, H, L, D, causal, description); bf16,
+# no rotary tables on either side.
+FLASH_WORKLOADS = {
+    "flash_c3": (8, 12, 4096, 64, True, "C3's shape without rotary tables, causal"),
+    "flash_tpu2k": (1, 8, 2048, 128, False, "the reference's TPU comparison shape, L=2048, non-causal"),
+    "flash_tpu4k": (1, 8, 4096, 128, False, "the reference's TPU comparison shape, L=4096, non-causal"),
+}
+
+
+def flash_bench(args, dev):
+    """pallas_afa_forward (this library) and torch's scaled_dot_product_attention restricted to its
+    flash backend, timed alike in one process on the same bf16 q, k, v.  The FLOPs of both are
+    4 B H D N_pairs, so the ratio is the time ratio.  As the reference does, a missing flash
+    kernel is recorded as unavailable rather than replaced by a dense softmax; torch's
+    memory-efficient fused kernel is timed beside it for context."""
+    import torch
+    import torch.nn.functional as F
+
+    import algebraic_intelligence_amd as A
+
+    B, H, L, D, causal, workload = FLASH_WORKLOADS[args.workload]
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn((B, H, L, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+               for _ in range(3))
+    stream = torch.cuda.current_stream(dev)
+    flops = A.afa_flops(B, H, L, D, causal=causal)
+
+    def timed(step):
+        warm = warm_up(step, args)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / args.steps
+        return {"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+                "warmup_run": {"steps": warm[0], "seconds": warm[1]}}
+
+    afa = timed(lambda: A.pallas_afa_forward(q, k, v, sink_omega=0.5, causal=causal))
+    others = {}
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        backends = {"flash": SDPBackend.FLASH_ATTENTION, "efficient": SDPBackend.EFFICIENT_ATTENTION}
+    except ImportError as e:  # pragma: no cover - torch without the selector
+        backends = {}
+        others["flash"] = {"available": False, "reason": f"torch.nn.attention: {e}"}
+    for name, be in backends.items():
+        def step(be=be):
+            with sdpa_kernel([be]):
+                return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+        try:
+            step()
+            torch.cuda.synchronize()
+        except Exception as e:  # the backend has no kernel for this GPU, dtype or shape
+            others[name] = {"available": False, "reason": f"{type(e).__name__}: {str(e)[:200]}"}
+            continue
+        others[name] = {"available": True, **timed(step)}
+    fl = others.get("flash", {})
+    ratio = round(fl["ms"] / afa["ms"], 4) if fl.get("available") else None
+    print(json.dumps({
+        "metric": f"AFA / softmax FlashAttention throughput ratio, same GPU [{args.workload}]",
+        "value": ratio, "unit": "ratio (AFA TFLOP/s / flash TFLOP/s)", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": afa["ms"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic: q,k,v ~ N(0,1) bf16, resident in HBM",
+        "config": {"workload": workload, "batch": B, "heads": H, "seq_len": L, "head_dim": D, "causal": causal,
+                   "flops_per_step": flops},
+        "afa": afa, "sdpa": others,
+        "efficient_ratio": (round(others["efficient"]["ms"] / afa["ms"], 4)
+                            if others.get("efficient", {}).get("available") else None),
+        "reference_bar": {"gate": 0.85, "tpu_v4_ratio": {"L2048": 0.9841, "L4096": 0.9967}},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -456,6 +601,9 @@ def main():
         return
     if args.workload in OACE_WORKLOADS:
         oace_bench(args, dev)
+        return
+    if args.workload in FLASH_WORKLOADS:
+        flash_bench(args, dev)
         return
     if args.workload in RING_WORKLOADS:
         ring_bench(args, dev)
@@ -588,6 +736,9 @@ def main():
             line["metric"] = line["metric"].replace("AFA fwd", "AFA bwd")
         if dt_name != "bf16":
             line["metric"] = line["metric"].replace("bf16 MFMA peak", f"{dt_name} MFMA peak")
+    if not args.no_power:
+        # board power and clocks under the same calls, sustained; run after the timed region
+        line["power"] = power_sample(step)
     if not args.no_cpu and args.workload == "c3":
         line["cpu_baseline"] = cpu_baseline(q, k, v, rot, args.cpu_seconds)
         line["cpu_baseline"]["gpu_speedup"] = round(tflops / line["cpu_baseline"]["value"], 1)
