@@ -109,9 +109,12 @@ def test_c3_fused_ago_full_size(dt):
     ct, st = O.cayley_tables(D, L, freqs=_c3_freqs(D))
     ref = O.afa_forward(to_f64(q[:1, :2]), to_f64(k[:1, :2]), to_f64(v[:1, :2]), 0.5, True, rotary=(ct, st))
     e_r = normwise(to_f64(out[:1, :2]), ref)
-    print(f"C3 {dt}: vs contract {e_c:.3e}, vs fp64 (2 heads) {e_r:.3e}")
+    e_d = normwise(to_f64(den), c_den)
+    print(f"C3 {dt}: vs contract {e_c:.3e}, denominator {e_d:.3e}, vs fp64 (2 heads) {e_r:.3e}")
     assert e_c <= _ulp_tol(dt) and e_r <= 2e-2
-    assert normwise(to_f64(den), c_den) <= 1e-4
+    # the kernel and the contract add the same fp32 weights of up to 4096 keys in different
+    # orders (lane partials and a tree against a sequential sum): measured 3e-6 to 4e-6
+    assert e_d <= 2e-5
 
 
 # ----------------------------------------------------------------------------------- invariants

@@ -69,13 +69,15 @@ def test_c4_full_size(dt, seed):
         e_r = max(e_r, normwise(to_f64(out[b, h]), ref))
         # bf16: the contract rounds the rotated q and k to bf16 before the dot (the reference's
         # _rotate_tensor works in the input dtype), float64 does not; the contract check above
-        # pins the denominator to 1e-4
+        # pins the denominator to 1e-5
         assert normwise(to_f64(den[b, h]), dref) <= (1e-5 if dt == torch.float32 else 2e-2)
     print(f"C4 {dt} seed {seed}: vs contract {e_c:.2e} (128 heads), denominator {e_d:.2e}, "
           f"vs fp64 {e_r:.2e} (2 heads)")
     assert np.isfinite(to_f64(out)).all()
     assert e_c <= _ulp_tol(dt)
-    assert e_d <= (1e-5 if dt == torch.float32 else 1e-4)
+    # both dtypes add the same fp32 weights of up to 1024 keys in another order than the contract:
+    # measured up to 1.9e-6 (fp32) and 1.3e-6 (bf16) over the eight seeds
+    assert e_d <= 1e-5
     assert e_r <= (1e-5 if dt == torch.float32 else 2e-2)
 
 
@@ -108,7 +110,10 @@ def test_c5_forward_full_length(c5):
         e_r = normwise(to_f64(out[b, h, :n]), ref)
         print(f"C5 forward head ({b},{h}): vs contract {e_c:.2e}, denominator {e_d:.2e}, "
               f"first {n} rows vs fp64 {e_r:.2e}")
-        assert e_c <= _ulp_tol(torch.bfloat16) and e_d <= 1e-4 and e_r <= 2e-2
+        # the denominator sums up to 8192 fp32 weights in another order than the contract
+        # (lane partials, a tree and a cross-lane add against a sequential sum): measured 6.3e-6
+        # and 6.9e-6
+        assert e_c <= _ulp_tol(torch.bfloat16) and e_d <= 3e-5 and e_r <= 2e-2
 
 
 def test_c5_backward_full_length(c5):
@@ -155,7 +160,8 @@ def test_key_split_matches_contract(shape, causal, valid, dt, rotary):
     print(f"{shape} causal={causal} valid={valid} {dt} rotary={rotary}: workspace {ws} B, vs contract {e:.2e}, "
           f"denominator {e_d:.2e}")
     assert np.isfinite(to_f64(out)).all()
-    assert e <= _ulp_tol(dt) and e_d <= 1e-4
+    # the split adds each part's fp32 row sums in part order: measured 1.1e-6 to 1.6e-6
+    assert e <= _ulp_tol(dt) and e_d <= 1e-5
     # the parts are added in part order whichever finishes last: calls are bit for bit repeatable
     out2, den2 = _fwd(q, k, v, causal=causal, valid=valid, rotary=rot)
     assert torch.equal(out, out2) and torch.equal(den, den2)
