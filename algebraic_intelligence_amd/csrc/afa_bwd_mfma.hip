@@ -22,7 +22,9 @@
 // Tiles of 64 rows are loaded by direct global -> LDS loads into two buffers; rows are D
 // elements with 16-byte chunks XOR-swizzled by (row & 7) (conflict-free 32-row fragments).
 // 1/sqrt(D) is split into 1/8 folded into the register-resident operand (exact) and the factor
-// 8 fl(1/sqrt D) applied to the fp32 score (the same rounding as s * scale; 1 at D = 64).
+// 8 fl(1/sqrt D) applied to the fp32 score (the same rounding as s * scale; 1 at D = 64); at
+// head_dim 128 in bf16, 1/16 is folded and the score factor sqrt 2 enters the rho^8 formula
+// instead (rho8r_half).
 // head_dim 32, 48 and 96 run as 64, 64 and 128: padding chunks of the LDS rows are direct-loaded
 // from a zero chunk in device memory, padding features of the register operands are zero, and
 // only the head_dim features of dq, dk, dv are stored.
@@ -147,6 +149,33 @@ __device__ __forceinline__ float rho8r(float s, float& r) {
   return p8;
 }
 
+// Head_dim 128 in bf16 folds 1/16 into the register-resident operand instead of 1/8, so the MFMA
+// forms x = s / sqrt(2) with no score multiply (1/sqrt(128) = 2^-4 / sqrt 2).  Then
+// rho(s) / sqrt 2 = x + sqrt(x^2 + 1/2), whose eighth power is rho(s)^8 / 16, and
+// rsqrt(1 + s^2) = rsqrt(x^2 + 1/2) / sqrt 2, so ds = 8 scale r w (dP - E) becomes
+// 8 rh (rho^8/16) (1/d) (dP - E) with rh = rsqrt(x^2 + 1/2): the powers of two go into 8/d (dQ)
+// or into the dk and dv stores (dK/dV: w / 16 and ds / 8 are exact scalings, rounded to bf16
+// the same way).  fp16 keeps the 1/8 fold: w / 16 would fall into its subnormals sooner.
+template <int DT, int D>
+constexpr bool half_form() { return D == 128 && DT == AFA_BF16; }
+template <int DT, int D>
+constexpr float fold_scale() { return half_form<DT, D>() ? 0.0625f : 0.125f; }
+
+// rho(s)^8 / 16 and rh = rsqrt(x^2 + 1/2) for s = sqrt(2) x.  EXACT: two-branch, rho(|s|)^8 / 16
+// for s >= 0 and 1 / (256 (rho(|s|)/sqrt 2)^8) = rho(s)^8 / 16 for s < 0 (rho(s) rho(-s) = 1).
+template <bool EXACT>
+__device__ __forceinline__ float rho8r_half(float x, float& rh) {
+  const float a = EXACT ? __builtin_fabsf(x) : x;
+  const float t = __builtin_fmaf(a, a, 0.5f);
+  rh = __builtin_amdgcn_rsqf(t);
+  const float rho = __builtin_fmaf(t, rh, a);
+  const float p2 = rho * rho;
+  const float p4 = p2 * p2;
+  const float p8 = p4 * p4;
+  if constexpr (EXACT) return x < 0.0f ? __builtin_amdgcn_rcpf(p8 * 256.0f) : p8;
+  return p8;
+}
+
 }  // namespace
 
 // Source of the padding chunks of LDS rows (head_dim 32, 48, 96).
@@ -264,11 +293,11 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
     qf[kc] = z;
     gf[kc] = z;
     if (qi < L && 16 * kc + 8 * g < D) {
-      qf[kc] = bscale<DT>(*(const u32x4_t*)(qp + (int64_t)qi * D + 16 * kc + 8 * g), 0.125f);
+      qf[kc] = bscale<DT>(*(const u32x4_t*)(qp + (int64_t)qi * D + 16 * kc + 8 * g), fold_scale<DT, D>());
       gf[kc] = *(const u32x4_t*)(gp + (int64_t)qi * D + 16 * kc + 8 * g);
     }
   }
-  // fast-rho guard: the largest squared norm of the wave's q / 8 rows against the key blocks
+  // fast-rho guard: the largest squared norm of the wave's scaled q rows against the key blocks
   bool fast = false;
   if (!EXACT) {
     float n2 = 0.0f;
@@ -281,6 +310,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   const int64_t prows = (int64_t)BH * LP;
   const float ei = qi < L ? ((const float*)a.e_ws)[(int64_t)bh * LP + qi] : 0.f;
   const float invd = qi < L ? ((const float*)a.e_ws)[prows + (int64_t)bh * LP + qi] : 0.f;
+  const float invd8 = 8.0f * invd;  // the half form's ds = rh (rho^8/16) (8/d) (dP - E)
 
   f32x16_t dq[NFB];
 #pragma unroll
@@ -360,10 +390,15 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
     float ds[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float s = S[r] * SQ;
       float rr;
-      const float w = rho8r<E>(s, rr) * invd;
-      ds[r] = C8 * rr * w * (P[r] - ei);
+      if constexpr (half_form<DT, D>()) {
+        const float w8 = rho8r_half<E>(S[r], rr) * invd8;
+        ds[r] = rr * w8 * (P[r] - ei);
+      } else {
+        const float s = S[r] * SQ;
+        const float w = rho8r<E>(s, rr) * invd;
+        ds[r] = C8 * rr * w * (P[r] - ei);
+      }
     }
     if (!CLEAN && need_mask(n)) {
 #pragma unroll
@@ -599,10 +634,16 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               const int r = 4 * r4 + u;
-              const float s = S[r] * SQ;
               float rr;
-              w[u] = rho8r<!FAST>(s, rr) * i4[u];
-              ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+              if constexpr (half_form<DT, D>()) {
+                // w / 16 and ds / 8: the dv and dk stores scale them back
+                w[u] = rho8r_half<!FAST>(S[r], rr) * i4[u];
+                ds[u] = rr * w[u] * (P[r] - e4[u]);
+              } else {
+                const float s = S[r] * SQ;
+                w[u] = rho8r<!FAST>(s, rr) * i4[u];
+                ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+              }
             }
             if (need_mask) {
               // a side effect the compiler cannot move keeps this a branch on the wave-uniform
@@ -703,10 +744,16 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               const int r = 4 * r4 + u;
-              const float s = S[r] * SQ;
               float rr;
-              w[u] = rho8r<!FAST>(s, rr) * i4[u];
-              ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+              if constexpr (half_form<DT, D>()) {
+                // w / 16 and ds / 8: the dv and dk stores scale them back
+                w[u] = rho8r_half<!FAST>(S[r], rr) * i4[u];
+                ds[u] = rr * w[u] * (P[r] - e4[u]);
+              } else {
+                const float s = S[r] * SQ;
+                w[u] = rho8r<!FAST>(s, rr) * i4[u];
+                ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+              }
             }
             if (need_mask) {
               // a side effect the compiler cannot move keeps this a branch on the wave-uniform
@@ -742,6 +789,9 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
   }
 
   if (kj < L) {
+    // the half form accumulated dk / 8 and dv / 16 (exact powers of two, undone at the pack)
+    constexpr float KS = half_form<DT, D>() ? 8.0f : 1.0f;
+    constexpr float VS = half_form<DT, D>() ? 16.0f : 1.0f;
     if (a.rc != nullptr) {  // k was rotated: dk = R^T (dL/d(Rk))
 #pragma unroll
       for (int fb = 0; fb < NFB; ++fb)
@@ -760,10 +810,10 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
         const int f = fb * 32 + r4 * 8 + 4 * g;  // features f .. f+3 (D is a multiple of 16)
         if (D == DP || f < D) {
           u32x2_t wk, wv;
-          wk[0] = Elem<DT>::pack(dk[fb][4 * r4 + 0], dk[fb][4 * r4 + 1]);
-          wk[1] = Elem<DT>::pack(dk[fb][4 * r4 + 2], dk[fb][4 * r4 + 3]);
-          wv[0] = Elem<DT>::pack(dv[fb][4 * r4 + 0], dv[fb][4 * r4 + 1]);
-          wv[1] = Elem<DT>::pack(dv[fb][4 * r4 + 2], dv[fb][4 * r4 + 3]);
+          wk[0] = Elem<DT>::pack(dk[fb][4 * r4 + 0] * KS, dk[fb][4 * r4 + 1] * KS);
+          wk[1] = Elem<DT>::pack(dk[fb][4 * r4 + 2] * KS, dk[fb][4 * r4 + 3] * KS);
+          wv[0] = Elem<DT>::pack(dv[fb][4 * r4 + 0] * VS, dv[fb][4 * r4 + 1] * VS);
+          wv[1] = Elem<DT>::pack(dv[fb][4 * r4 + 2] * VS, dv[fb][4 * r4 + 3] * VS);
           *(u32x2_t*)(kout + f) = wk;
           *(u32x2_t*)(vout + f) = wv;
         }
@@ -818,7 +868,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
     u32x4_t z = {0u, 0u, 0u, 0u};
     kf[kc] = z;
     if (kj < L && 16 * kc + 8 * g < D) {
-      kf[kc] = bscale<DT>(*(const u32x4_t*)(kp + (int64_t)kj * D + 16 * kc + 8 * g), 0.125f);
+      kf[kc] = bscale<DT>(*(const u32x4_t*)(kp + (int64_t)kj * D + 16 * kc + 8 * g), fold_scale<DT, D>());
     }
   }
   {
@@ -836,7 +886,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       lds_dma16(vs, &lds_vk[(256 * i + wave * 64) * 8]);
     }
   }
-  // fast-rho guard: the largest squared norm of the wave's k / 8 rows against the query blocks
+  // fast-rho guard: the largest squared norm of the wave's scaled k rows against the query blocks
   bool fast = false;
   if (!EXACT) {
     float n2 = 0.0f;
@@ -888,8 +938,9 @@ static hipError_t bwd_launch(GenArgs a, void* rot_scratch, hipStream_t st) {
     if (e == hipSuccess) e = rownorm_launch(DT, a.k, sb, sh, sl, a.B, a.H, a.L, a.D, (float*)a.kbm, st);
     if (e != hipSuccess) return e;
     a.nkb = (a.L + 63) / 64;
-    // dQ forms s = S * score_factor with q / 8 and k as stored (dK/dV: q and k / 8)
-    a.nb_lim = fast_rho_lim(D == 64 ? 1.0 : D == 128 ? 0.70710677 : 8.0 * a.scale);
+    // dQ forms s = S * score_factor with q / 8 and k as stored (dK/dV: q and k / 8); the half
+    // form forms x = s / sqrt 2 from q / 16 (k / 16)
+    a.nb_lim = fast_rho_lim(D == 64 ? 1.0 : half_form<DT, D>() ? 1.4142135623730951 : D == 128 ? 0.70710677 : 8.0 * a.scale);
   } else {
     a.qbm = a.kbm = nullptr;
   }
