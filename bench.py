@@ -103,8 +103,9 @@ def warm_up(step, args):
 def power_sample(step, seconds=1.5):
     """Run `step` back to back for `seconds` while sampling the board with amd-smi: the socket
     power (W) and the current clock of each XCD's graphics domain (MHz), as medians over the
-    samples.  MI355X's board power limit is 1400 W; a workload drawing that much runs below the
-    2.4 GHz maximum clock, and the dense MFMA peak assumes the maximum."""
+    samples.  The dense MFMA peak assumes the 2.4 GHz maximum clock; under MFMA-dense work the
+    board holds less (the clock falls with the density of MFMA work, also below the 1400 W board
+    power limit)."""
     import re
     import shutil
     import subprocess
