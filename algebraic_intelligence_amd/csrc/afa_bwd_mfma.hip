@@ -9,7 +9,7 @@
 // Three launches (four with rotary tables), no atomics:
 //   * afa_bwd_mfma_rotate_kernel (rotary tables only): q and k rotated once into scratch; dq and
 //     dk are rotated back through R^T in the dQ / dK store epilogues;
-//   * afa_bwd_mfma_prep_kernel: E_i and 1/d_i per row into the workspace;
+//   * afa_bwd_mfma_prep_kernel: -E_i and 1/d_i per row into the workspace;
 //   * afa_bwd_mfma_dq_kernel (one lane per query, like the forward): S^T = K Q^T, dP^T = V g^T on
 //     MFMA, W and dS on the VALU, dQ^T += K^T dS^T with K^T read from the same LDS tile by
 //     ds_read_tr16_b64;
@@ -185,9 +185,10 @@ __device__ __attribute__((aligned(16))) unsigned int afa_bwd_zero_chunk[4];
 // 1/d lies inside one head (the dK/dV kernel loads them 4 rows at a time).
 __host__ __device__ constexpr int ws_rows(int L) { return (L + 3) & ~3; }
 
-// E_i = sum_d g_id out_id and 1/d_i per row: 8 lanes per row, 16-byte chunks of g and out.
-// Workspace layout: E at [bh * LP + i], 1/d at [B H LP + bh * LP + i], LP = ws_rows(L); the
-// padding rows hold zeros.
+// -E_i = -sum_d g_id out_id and 1/d_i per row: 8 lanes per row, 16-byte chunks of g and out.
+// Workspace layout: -E at [bh * LP + i], 1/d at [B H LP + bh * LP + i], LP = ws_rows(L); the
+// padding rows hold zeros.  E is stored negated because the dK/dV kernel starts its dP
+// accumulators from it (dP - E out of the MFMA) and the dQ kernel adds it in an fma.
 template <int DT>
 __global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a) {
   const int LP = ws_rows(a.L);
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void afa_bwd_mfma_prep_kernel(const GenArgs a)
   part += __shfl_xor(part, 2);
   part += __shfl_xor(part, 4);
   if (prow < prows && sub == 0) {
-    ((float*)a.e_ws)[prow] = live ? part : 0.f;
+    ((float*)a.e_ws)[prow] = live ? -part : 0.f;
     ((float*)a.e_ws)[prows + prow] = live ? 1.0f / ((const float*)a.dtot)[row] : 0.f;
   }
 }
@@ -308,9 +309,12 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   }
   const int LP = ws_rows(L);
   const int64_t prows = (int64_t)BH * LP;
-  const float ei = qi < L ? ((const float*)a.e_ws)[(int64_t)bh * LP + qi] : 0.f;
+  const float nei = qi < L ? ((const float*)a.e_ws)[(int64_t)bh * LP + qi] : 0.f;  // -E
   const float invd = qi < L ? ((const float*)a.e_ws)[prows + (int64_t)bh * LP + qi] : 0.f;
-  const float invd8 = 8.0f * invd;  // the half form's ds = rh (rho^8/16) (8/d) (dP - E)
+  // ds = r rho^8 (f dP + c) with the query's f = 8 scale / d and c = -E f: one fma per score for
+  // the factor (8 scale / d)(dP - E).  The half form's f is 8 / d: ds = rh (rho^8/16) (8/d)(dP - E)
+  const float fq = half_form<DT, D>() ? 8.0f * invd : C8 * invd;
+  const float cq = nei * fq;
 
   f32x16_t dq[NFB];
 #pragma unroll
@@ -392,12 +396,11 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
     for (int r = 0; r < 16; ++r) {
       float rr;
       if constexpr (half_form<DT, D>()) {
-        const float w8 = rho8r_half<E>(S[r], rr) * invd8;
-        ds[r] = rr * w8 * (P[r] - ei);
+        const float p8 = rho8r_half<E>(S[r], rr);
+        ds[r] = (rr * p8) * __builtin_fmaf(P[r], fq, cq);
       } else {
-        const float s = S[r] * SQ;
-        const float w = rho8r<E>(s, rr) * invd;
-        ds[r] = C8 * rr * w * (P[r] - ei);
+        const float p8 = rho8r<E>(S[r] * SQ, rr);
+        ds[r] = (rr * p8) * __builtin_fmaf(P[r], fq, cq);
       }
     }
     if (!CLEAN && need_mask(n)) {
@@ -483,7 +486,7 @@ struct DkdvLds {
   static constexpr int QT = DP >= 128 ? 32 : 64;
   unsigned short q[2][QT * DP];
   unsigned short g[2][QT * DP];
-  float ei[2][2 * QT];  // E then 1/d of the tile's rows
+  float ei[2][2 * QT];  // -E then 1/d of the tile's rows
   unsigned short vk[128 * DP];
 };
 
@@ -577,7 +580,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
     }
     }
     if (wave == 0 && lane < 2 * LPE) {
-      // LPE lanes of E, LPE of 1/d: 4 rows per lane (the head's LP rows are a whole number of
+      // LPE lanes of -E, LPE of 1/d: 4 rows per lane (the head's LP rows are a whole number of
       // chunks; rows in [L, LP) hold zeros); chunks past LP re-read the last one (masked rows)
       const int rr = t * QT + (lane % LPE) * 4;
       const int r0 = rr < LP ? rr : LP - 4;
@@ -609,9 +612,14 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           const int rq = sub * 32 + l32;
           f32x16_t S, P;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            S[e] = 0.f;
-            P[e] = 0.f;
+          for (int e = 0; e < 16; ++e) S[e] = 0.f;
+          // dP starts from -E of its query rows (element 4 r4 + u: tile row sub 32 + 8 r4 + 4 g + u),
+          // so the MFMA chain leaves dP - E
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x4_t ne4 = *(const f32x4_t*)(tei + sub * 32 + r4 * 8 + 4 * g);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) P[4 * r4 + u] = ne4[u];
           }
 #pragma unroll
           for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
@@ -628,7 +636,6 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
             const int lr = sub * 32 + r4 * 8 + 4 * g;  // tile row of element 4 r4
-            const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
             const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
             float w[4], ds[4];
 #pragma unroll
@@ -638,11 +645,11 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
               if constexpr (half_form<DT, D>()) {
                 // w / 16 and ds / 8: the dv and dk stores scale them back
                 w[u] = rho8r_half<!FAST>(S[r], rr) * i4[u];
-                ds[u] = rr * w[u] * (P[r] - e4[u]);
+                ds[u] = rr * w[u] * P[r];
               } else {
                 const float s = S[r] * SQ;
                 w[u] = rho8r<!FAST>(s, rr) * i4[u];
-                ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+                ds[u] = C8 * rr * w[u] * P[r];
               }
             }
             if (need_mask) {
@@ -720,9 +727,14 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           const int rq = sub * 32 + l32;
           f32x16_t S, P;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            S[e] = 0.f;
-            P[e] = 0.f;
+          for (int e = 0; e < 16; ++e) S[e] = 0.f;
+          // dP starts from -E of its query rows (element 4 r4 + u: tile row sub 32 + 8 r4 + 4 g + u),
+          // so the MFMA chain leaves dP - E
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x4_t ne4 = *(const f32x4_t*)(tei + sub * 32 + r4 * 8 + 4 * g);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) P[4 * r4 + u] = ne4[u];
           }
 #pragma unroll
           for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
@@ -738,7 +750,6 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
             const int lr = sub * 32 + r4 * 8 + 4 * g;  // tile row of element 4 r4
-            const f32x4_t e4 = *(const f32x4_t*)(tei + lr);
             const f32x4_t i4 = *(const f32x4_t*)(tei + QT + lr);
             float w[4], ds[4];
 #pragma unroll
@@ -748,11 +759,11 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
               if constexpr (half_form<DT, D>()) {
                 // w / 16 and ds / 8: the dv and dk stores scale them back
                 w[u] = rho8r_half<!FAST>(S[r], rr) * i4[u];
-                ds[u] = rr * w[u] * (P[r] - e4[u]);
+                ds[u] = rr * w[u] * P[r];
               } else {
                 const float s = S[r] * SQ;
                 w[u] = rho8r<!FAST>(s, rr) * i4[u];
-                ds[u] = C8 * rr * w[u] * (P[r] - e4[u]);
+                ds[u] = C8 * rr * w[u] * P[r];
               }
             }
             if (need_mask) {
