@@ -109,6 +109,51 @@ __device__ __forceinline__ u32x4_t frag_tr(const unsigned short* tile, int r0, i
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
 constexpr int padded_dim(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
+
+// Layout of the dK/dV kernel's q and g tiles at head_dim 128: each row is padded to 320 bytes
+// (20 chunk slots) and the chunks of each 64-byte group are XOR-swizzled by (r >> 2) & 3.  A row
+// starts 16 banks after the previous one, so the 4 rows of a transposed read's 32-lane pass fall
+// in 4 different 16-bank groups and the 16 rows of a row read's pass in 16 different 4-bank
+// quads (no conflicts).  The offsets of different 64-byte groups (fb, kc / 2) and of rows a
+// multiple of 16 apart differ by constants (qg_additive), so each read of a tile is one of four
+// lane offsets plus an immediate: two for the row reads (kc even or odd), two for the transposed
+// reads (their two 8-row halves).  Other head dims keep the swizzle of the other tiles.
+constexpr int qg_pitch(int d) { return d == 128 ? 160 : padded_dim(d); }
+
+__host__ __device__ constexpr int qg_off128(int r, int c) {
+  return r * 160 + ((4 * (c >> 2) + ((c & 3) ^ ((r >> 2) & 3))) << 3);
+}
+
+// Element offset of the row read (chunk 2 kc + g of row 32 sub + l32) and of the half-hh
+// transposed read (frag_tr's rows r0 + 8 hh + 4 g + l16 / 4, column block fb, r0 = 32 sub + 16 kk)
+// on a padded tile.
+__host__ __device__ constexpr int qg_row_off(int sub, int kc, int l32, int g) {
+  return qg_off128(sub * 32 + l32, 2 * kc + g);
+}
+__host__ __device__ constexpr int qg_tr_off(int r0, int fb, int hh, int g, int l16, int m16) {
+  return qg_off128(r0 + hh * 8 + 4 * g + (l16 >> 2), (fb * 32 + m16 * 16 + 4 * (l16 & 3)) >> 3) +
+         ((4 * (l16 & 3)) & 7);
+}
+
+// Every row read equals its lane's offset for (sub 0, kc & 1) plus sub * 32 rows plus 32 (kc / 2)
+// elements, and every transposed read its lane's offset for (r0 0, fb 0) plus r0 rows plus
+// 32 fb elements: the reads below rely on it.
+constexpr bool qg_additive() {
+  for (int lane = 0; lane < 64; ++lane) {
+    const int l32 = lane & 31, g = lane >> 5, l16 = lane & 15, m16 = (lane >> 4) & 1;
+    for (int sub = 0; sub < 1; ++sub)
+      for (int kc = 0; kc < 8; ++kc)
+        if (qg_row_off(sub, kc, l32, g) != qg_row_off(0, kc & 1, l32, g) + sub * 32 * 160 + 32 * (kc >> 1))
+          return false;
+    for (int r0 = 0; r0 < 32; r0 += 16)
+      for (int fb = 0; fb < 4; ++fb)
+        for (int hh = 0; hh < 2; ++hh)
+          if (qg_tr_off(r0, fb, hh, g, l16, m16) != qg_tr_off(0, 0, hh, g, l16, m16) + r0 * 160 + 32 * fb)
+            return false;
+  }
+  return true;
+}
+static_assert(qg_additive(), "padded q/g tile offsets must be lane offset + constant");
 // Waves per SIMD of the dQ and dK/dV kernels by padded head dim.
 constexpr int bwd_waves(int dp) { return dp == 64 ? 3 : dp == 128 ? 2 : 1; }
 
@@ -481,11 +526,11 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
 // ------------------------------------------------------------------------------ dK, dV
 // LDS of the dK/dV kernel: double-buffered q and g tiles of QT rows, E and 1/d of the tile rows,
 // and the V rows of the workgroup's 128 keys.
-template <int DP>
+template <int DP, int PITCH>
 struct DkdvLds {
   static constexpr int QT = DP >= 128 ? 32 : 64;
-  unsigned short q[2][QT * DP];
-  unsigned short g[2][QT * DP];
+  unsigned short q[2][QT * PITCH];
+  unsigned short g[2][QT * PITCH];
   float ei[2][2 * QT];  // -E then 1/d of the tile's rows
   unsigned short vk[128 * DP];
 };
@@ -494,7 +539,7 @@ struct DkdvLds {
 // branch-free form, the wave's scores all within the fast-rho bound); the kernel instantiates
 // both and each wave runs one, so the two loops get their own register allocation.
 template <int DT, int D, bool FAST>
-__device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D)>& lds,
+__device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D), qg_pitch(D)>& lds,
                                           const u32x4_t (&kf)[padded_dim(D) / 16], int bh, int kblk) {
   constexpr int DP = padded_dim(D);
   // The V rows of the workgroup's 128 keys stay in LDS instead of registers.  At DP = 128 (where
@@ -551,6 +596,24 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       const uint32_t s0 = __builtin_amdgcn_readfirstlane((uint32_t)(t * QT * D) * 2u);
       const i32x4_t qsrd = raw_buffer_srd_at(qp, (uint32_t)(L * D) * 2u, s0);
       const i32x4_t gsrd = raw_buffer_srd_at(gp, (uint32_t)(L * D) * 2u, s0);
+      if constexpr (D == 128) {
+        // QT rows of 20 slots (qg_off): slot s = tid + 256 i holds chunk c of row s / 20; each
+        // wave's instruction fills 64 consecutive slots, and the 4 padding slots of a row re-read
+        // the row's first chunk (in bounds, never read back).  Waves whose slots all lie past the
+        // tile skip the last instruction (every wait here is for all loads).
+        constexpr int SLOTS = QT * 20;
+#pragma unroll
+        for (int i = 0; i < (SLOTS + 255) / 256; ++i) {
+          if (256 * i + 64 * wave < SLOTS) {
+            const int sl = tid + 256 * i;
+            const int row = sl / 20, cp = sl - row * 20;
+            const int c = cp < 16 ? 4 * (cp >> 2) + ((cp & 3) ^ ((row >> 2) & 3)) : 0;
+            const uint32_t off = (uint32_t)(row * D + c * 8) * 2u;
+            lds_dma16_buf(qsrd, off, &lds_q[t & 1][(256 * i + wave * 64) * 8]);
+            lds_dma16_buf(gsrd, off, &lds_g[t & 1][(256 * i + wave * 64) * 8]);
+          }
+        }
+      } else {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int c = tid + 256 * i;
@@ -559,6 +622,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
         const uint32_t off = (uint32_t)(row * D + lc * 8) * 2u;
         lds_dma16_buf(qsrd, off, &lds_q[t & 1][(256 * i + wave * 64) * 8]);
         lds_dma16_buf(gsrd, off, &lds_g[t & 1][(256 * i + wave * 64) * 8]);
+      }
       }
     } else {
 #pragma unroll
@@ -586,6 +650,36 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       const int r0 = rr < LP ? rr : LP - 4;
       const float* src = (lane < LPE ? ep : ip) + r0;
       lds_dma16(src, &lds_ei[t & 1][0]);
+    }
+  };
+
+  // q and g tile reads: at head_dim 128 one of four lane offsets plus an immediate (qg_additive)
+  int qro[2] = {0, 0}, qto[2] = {0, 0};
+  if constexpr (D == 128) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      qro[h] = qg_row_off(0, h, l32, g);
+      qto[h] = qg_tr_off(0, 0, h, g, l16, m16);
+    }
+  }
+  auto qg_row = [&](const unsigned short* tile, int sub, int kc) -> u32x4_t {
+    if constexpr (D == 128) return *(const u32x4_t*)(tile + qro[kc & 1] + sub * 32 * 160 + 32 * (kc >> 1));
+    else return frag_row<DP>(tile, sub * 32 + l32, 2 * kc + g);
+  };
+  auto qg_tr = [&](const unsigned short* tile, int sub, int kk, int fb) -> u32x4_t {
+    if constexpr (D == 128) {
+      u32x4_t f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const unsigned short* p = tile + qto[hh] + (sub * 32 + kk * 16) * 160 + 32 * fb;
+        const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+        const u32x2_t w = __builtin_bit_cast(u32x2_t, v);
+        f[2 * hh] = w[0];
+        f[2 * hh + 1] = w[1];
+      }
+      return f;
+    } else {
+      return frag_tr<DP>(tile, sub * 32 + kk * 16, fb, g, l16, m16);
     }
   };
 
@@ -622,11 +716,11 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
             for (int u = 0; u < 4; ++u) P[4 * r4 + u] = ne4[u];
           }
 #pragma unroll
-          for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
+          for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(qg_row(tq, sub, kc), kf[kc], S);
 #pragma unroll
           for (int kc = 0; kc < NKC; ++kc) {
             const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
-            P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vk, P);
+            P = bmma<DT>(qg_row(tg, sub, kc), vk, P);
           }
           // W and dS, masked and packed to the element type four rows at a time (only those four
           // fp32 pairs are live next to the accumulators)
@@ -676,8 +770,8 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-              dv[fb] = bmma<DT>(frag_tr<DP>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
-              dk[fb] = bmma<DT>(frag_tr<DP>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
+              dv[fb] = bmma<DT>(qg_tr(tg, sub, kk, fb), wp[kk], dv[fb]);
+              dk[fb] = bmma<DT>(qg_tr(tq, sub, kk, fb), dsp[kk], dk[fb]);
             }
         }
       }
@@ -737,11 +831,11 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
             for (int u = 0; u < 4; ++u) P[4 * r4 + u] = ne4[u];
           }
 #pragma unroll
-          for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tq, rq, 2 * kc + g), kf[kc], S);
+          for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(qg_row(tq, sub, kc), kf[kc], S);
 #pragma unroll
           for (int kc = 0; kc < NKC; ++kc) {
             const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
-            P = bmma<DT>(frag_row<DP>(tg, rq, 2 * kc + g), vk, P);
+            P = bmma<DT>(qg_row(tg, sub, kc), vk, P);
           }
           // W and dS, masked and packed to the element type four rows at a time (only those four
           // fp32 pairs are live next to the accumulators)
@@ -788,8 +882,8 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-              dv[fb] = bmma<DT>(frag_tr<DP>(tg, sub * 32 + kk * 16, fb, g, l16, m16), wp[kk], dv[fb]);
-              dk[fb] = bmma<DT>(frag_tr<DP>(tq, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dk[fb]);
+              dv[fb] = bmma<DT>(qg_tr(tg, sub, kk, fb), wp[kk], dv[fb]);
+              dk[fb] = bmma<DT>(qg_tr(tq, sub, kk, fb), dsp[kk], dk[fb]);
             }
         }
       }
@@ -847,7 +941,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   constexpr int CPT = QT * NCK / 256;
   constexpr int NKC = DP / 16;
   constexpr int NFB = DP / 32;
-  __shared__ __attribute__((aligned(16))) DkdvLds<DP> lds;
+  __shared__ __attribute__((aligned(16))) DkdvLds<DP, qg_pitch(D)> lds;
   auto& lds_vk = lds.vk;
 
   const int tid = threadIdx.x;
