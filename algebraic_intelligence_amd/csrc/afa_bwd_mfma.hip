@@ -331,6 +331,10 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   const unsigned short* vp = (const unsigned short*)a.v + base;
   const unsigned short* gp = (const unsigned short*)a.g + base;
   const int qi = q0_w + l32;
+  // the fast-rho guard's key-block bounds go out first: they do not depend on q
+  const float* kbm = !EXACT && a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr;
+  const int kblk1 = (kend_w + 63) / 64;
+  const float kbm_first = fast_rho_prefetch(kbm, 0, kblk1);
 
   u32x4_t qf[NKC], gf[NKC];
 #pragma unroll
@@ -349,8 +353,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
     float n2 = 0.0f;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) n2 += chunk_norm2<DT>(qf[kc]);
-    fast = fast_rho_safe(a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr, 0, (kend_w + 63) / 64,
-                         wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim);
+    fast = fast_rho_safe(kbm, 0, kblk1, wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim, kbm_first);
   }
   const int LP = ws_rows(L);
   const int64_t prows = (int64_t)BH * LP;
@@ -967,6 +970,11 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   const float* ep = (const float*)a.e_ws + (int64_t)bh * LP;
   const float* ip = (const float*)a.e_ws + (int64_t)BH * LP + (int64_t)bh * LP;
 
+  // the fast-rho guard's query-block bounds go out first: they do not depend on k
+  const float* qbm = !EXACT && a.qbm != nullptr ? a.qbm + (int64_t)bh * a.nkb : nullptr;
+  const int qblk0 = t0 * QT / 64, qblk1 = (L + 63) / 64;
+  const float qbm_first = fast_rho_prefetch(qbm, qblk0, qblk1);
+
   u32x4_t kf[NKC];
 #pragma unroll
   for (int kc = 0; kc < NKC; ++kc) {
@@ -997,8 +1005,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
     float n2 = 0.0f;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) n2 += chunk_norm2<DT>(kf[kc]);
-    fast = fast_rho_safe(a.qbm != nullptr ? a.qbm + (int64_t)bh * a.nkb : nullptr, t0 * QT / 64, (L + 63) / 64,
-                         wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim);
+    fast = fast_rho_safe(qbm, qblk0, qblk1, wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim, qbm_first);
   }
   // head_dim 256 (one wave per SIMD, every accumulator in AGPRs, ~120 VGPRs spilled) takes the
   // two-branch form only: its instantiation holding both bodies returned wrong dv on the GPU

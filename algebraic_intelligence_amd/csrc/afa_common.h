@@ -289,6 +289,29 @@ __device__ __forceinline__ bool fast_rho_safe(const float* nb2, int blk0, int bl
   return ok;
 }
 
+// The first 64 bounds of fast_rho_safe's range, one per lane.  They do not depend on the rows
+// they are compared with, so a kernel loads them before its q (or k) loads and the guard waits
+// for one memory round trip instead of two.
+__device__ __forceinline__ float fast_rho_prefetch(const float* nb2, int blk0, int blk1) {
+  const int j = blk0 + (int)(threadIdx.x & 63);
+  return nb2 != nullptr && j < blk1 ? nb2[j] : 0.0f;
+}
+
+// fast_rho_safe with the range's first 64 bounds already loaded (fast_rho_prefetch); the same
+// result.
+__device__ __forceinline__ bool fast_rho_safe(const float* nb2, int blk0, int blk1, float vmax2, float lim,
+                                              float first) {
+  if (nb2 == nullptr) return false;
+  if (blk0 >= blk1) return true;
+  bool ok = __ballot(!(first * vmax2 <= lim)) == 0;
+  for (int base = blk0 + 64; base < blk1; base += 64) {
+    const int j = base + (int)(threadIdx.x & 63);
+    const float m = j < blk1 ? nb2[j] : 0.0f;
+    ok = ok && __ballot(!(m * vmax2 <= lim)) == 0;
+  }
+  return ok;
+}
+
 // Reference-faithful double precision evaluation (two branches, IEEE sqrt and division).
 __device__ __forceinline__ double rho8_f64(double s) {
   const double rad = 1.0 + s * s;

@@ -478,6 +478,10 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
   const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 256)) : vlen;
   const int kend_w = a.causal ? min(vlen, q0_w + 64) : vlen;
   const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
+  // the fast-rho guard's key-block bounds go out first: they do not depend on q
+  const float* kbm = !EXACT && a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr;
+  const int kblk1 = (kend_w + 63) / 64;
+  const float kbm_first = fast_rho_prefetch(kbm, 0, kblk1);
 
   // ---- Q fragments: query q0_w + qb*32 + l32, features kc*16 + 8g .. +7 (scaled, rotated)
   u32x4_t qf[2][4];
@@ -513,8 +517,7 @@ void afa_fwd_d64_kernel(const FwdArgs a) {
       for (int kc = 0; kc < 4; ++kc) n2 += chunk_norm2<DT>(qf[qb][kc]);
       m = __builtin_fmaxf(m, n2 + __shfl_xor(n2, 32));
     }
-    fast = fast_rho_safe(a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr, 0, (kend_w + 63) / 64,
-                         wave_max(m), a.nb_lim);
+    fast = fast_rho_safe(kbm, 0, kblk1, wave_max(m), a.nb_lim, kbm_first);
   }
   if (fast) d64_body<DT, true>(a, lds_k, lds_v, qf, bh, qblk);
   else d64_body<DT, false>(a, lds_k, lds_v, qf, bh, qblk);

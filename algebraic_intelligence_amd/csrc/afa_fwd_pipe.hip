@@ -583,6 +583,10 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
   const int kend_wg = a.causal ? min(vlen, min(L, q0_wg + 128)) : vlen;
   const int kend_w = a.causal ? min(vlen, q0_w + 32) : vlen;
   const unsigned short* qp = (const unsigned short*)a.q + b * a.q_b + h * a.q_h;
+  // the fast-rho guard's key-block bounds go out first: they do not depend on q
+  const float* kbm = !EXACT && a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr;
+  const int kblk1 = (kend_w + 63) / 64;
+  const float kbm_first = fast_rho_prefetch(kbm, 0, kblk1);
 
   // the first tiles of this workgroup's key range go out before the q loads, so that their
   // memory latencies overlap (pipe_body waits for them)
@@ -616,8 +620,7 @@ void afa_fwd_pipe_kernel(const FwdArgs a) {
     float n2 = 0.0f;
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) n2 += chunk_norm2<DT>(qf[kc]);
-    fast = fast_rho_safe(a.kbm != nullptr ? a.kbm + (int64_t)bh * a.nkb : nullptr, 0, (kend_w + 63) / 64,
-                         wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim);
+    fast = fast_rho_safe(kbm, 0, kblk1, wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim, kbm_first);
   }
 
   if (fast) pipe_body<D, DT, true, SM>(a, lds_k, lds_v, qf, bh, qblk, pp);
