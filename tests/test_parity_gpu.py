@@ -4,7 +4,8 @@
   in fp32 and bf16: every head against the C restatement of the dtype contract, two heads per
   seed against float64 (scripts/run_phase6_tpu.py:54-144, scripts/phase6_experiments.py:66-132).
 * C5 (B=2 H=16 L=8192 D=128, bf16, causal) forward and backward at full length against the
-  contract on two heads, and the first 2048 rows against float64.
+  contract on two heads, the first 2048 rows against float64, and 36 rows spread over the whole
+  length against float64 (out, d, dq of those query rows; dk, dv of those key rows).
 * tiled_afa_forward against float64 with valid_seq_len and return_denominator
   (src/kernels/pallas_afa.py:330-406).
 * The denominator of the bf16 path is the fp32 row sum of the unrounded weights
@@ -130,6 +131,41 @@ def test_c5_backward_full_length(c5):
             print(f"C5 backward head ({b},{h}) {name}: vs contract {e:.2e}")
             assert np.isfinite(to_f64(got[sl])).all()
             assert e <= 1e-2, name
+
+
+# rows spread over the whole length: the first and last, the 2048 boundary, and 28 more drawn
+# once with a fixed seed
+C5_ROWS = sorted({0, 1, 2047, 2048, 4095, 4096, 8190, 8191} |
+                 set(np.random.default_rng(5).integers(0, 8192, 28).tolist()))
+
+
+def test_c5_long_rows_fp64(c5):
+    """Full-length rows of C5 against float64 (tests/helpers.py: afa_rows_forward64 and
+    afa_rows_backward64, pinned against the oracle on the CPU): out and d of the sampled query
+    rows, each over all its keys up to 8192; dq of the same rows and dk, dv of the same key rows,
+    the key rows summed over all queries after them, from the GPU's own out and d as the
+    backward takes them."""
+    from tests.helpers import afa_rows_backward64, afa_rows_forward64
+
+    q, k, v, g, out, den, dq, dk, dv = c5
+    rows = C5_ROWS
+    for b, h in C5_HEADS:
+        qh, kh, vh, gh = (to_f64(t[b, h]) for t in (q, k, v, g))
+        o_r, d_r = afa_rows_forward64(qh, kh, vh, rows)
+        e_o = normwise(to_f64(out[b, h])[rows], o_r)
+        e_d = float(np.max(np.abs(den[b, h, rows, 0].double().cpu().numpy() - d_r) / d_r))
+        oh = to_f64(out[b, h])
+        dh = den[b, h, :, 0].double().cpu().numpy()
+        rq, rk, rv = afa_rows_backward64(qh, kh, vh, gh, oh, dh, rows, rows)
+        e_q = normwise(to_f64(dq[b, h])[rows], rq)
+        e_k = normwise(to_f64(dk[b, h])[rows], rk)
+        e_v = normwise(to_f64(dv[b, h])[rows], rv)
+        print(f"C5 head ({b},{h}), {len(rows)} full-length rows vs fp64: out {e_o:.2e}, d {e_d:.2e} (max rel), "
+              f"dq {e_q:.2e}, dk {e_k:.2e}, dv {e_v:.2e}")
+        # measured: out 2.9e-3 and 3.7e-3, d 4.9e-7 and 5.7e-7, dq / dk / dv 2.6e-3 to 3.2e-3 (the bf16
+        # rounding of the outputs and of the P, W and dS operands); bounds about four times that
+        assert e_o <= 1.5e-2 and e_d <= 3e-6
+        assert max(e_q, e_k, e_v) <= 1.5e-2
 
 
 # ----------------------------------------------------------------------------------- key split
