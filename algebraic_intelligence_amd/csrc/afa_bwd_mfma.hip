@@ -110,7 +110,8 @@ typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
 constexpr int padded_dim(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
-// Layout of the dK/dV kernel's q and g tiles at head_dim 128: each row is padded to 320 bytes
+// Layout of the dQ kernel's K and V tiles and of the dK/dV kernel's q and g tiles at head_dim 128:
+// each row is padded to 320 bytes
 // (20 chunk slots) and the chunks of each 64-byte group are XOR-swizzled by (r >> 2) & 3.  A row
 // starts 16 banks after the previous one, so the 4 rows of a transposed read's 32-lane pass fall
 // in 4 different 16-bank groups and the 16 rows of a row read's pass in 16 different 4-bank
@@ -141,11 +142,11 @@ __host__ __device__ constexpr int qg_tr_off(int r0, int fb, int hh, int g, int l
 constexpr bool qg_additive() {
   for (int lane = 0; lane < 64; ++lane) {
     const int l32 = lane & 31, g = lane >> 5, l16 = lane & 15, m16 = (lane >> 4) & 1;
-    for (int sub = 0; sub < 1; ++sub)
+    for (int sub = 0; sub < 2; ++sub)
       for (int kc = 0; kc < 8; ++kc)
         if (qg_row_off(sub, kc, l32, g) != qg_row_off(0, kc & 1, l32, g) + sub * 32 * 160 + 32 * (kc >> 1))
           return false;
-    for (int r0 = 0; r0 < 32; r0 += 16)
+    for (int r0 = 0; r0 < 64; r0 += 16)
       for (int fb = 0; fb < 4; ++fb)
         for (int hh = 0; hh < 2; ++hh)
           if (qg_tr_off(r0, fb, hh, g, l16, m16) != qg_tr_off(0, 0, hh, g, l16, m16) + r0 * 160 + 32 * fb)
@@ -309,8 +310,9 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   constexpr int NFB = DP / 32;
   const float SQ = score_factor<D>(a);  // score factor after the folded 1/8
   const float C8 = SQ;                  // 8 * scale
-  __shared__ __attribute__((aligned(16))) unsigned short lds_k[2][KT * DP];
-  __shared__ __attribute__((aligned(16))) unsigned short lds_v[2][KT * DP];
+  // at head_dim 128, rows padded to 320 bytes (qg_off128): 80 KB, two workgroups fill a CU's LDS
+  __shared__ __attribute__((aligned(16))) unsigned short lds_k[2][KT * qg_pitch(D)];
+  __shared__ __attribute__((aligned(16))) unsigned short lds_v[2][KT * qg_pitch(D)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -382,6 +384,22 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       const uint32_t s0 = (uint32_t)(t * KT * D) * 2u;
       const i32x4_t ksrd = raw_buffer_srd_at(kp, (uint32_t)(L * D) * 2u, s0);
       const i32x4_t vsrd = raw_buffer_srd_at(vp, (uint32_t)(L * D) * 2u, s0);
+      if constexpr (D == 128) {
+        // KT rows of 20 slots (qg_off128): slot sl = tid + 256 i holds chunk c of row sl / 20, each
+        // wave's instruction fills 64 consecutive slots, and a row's 4 padding slots re-read its
+        // first chunk (in bounds, never read back)
+        static_assert(KT * 20 % 256 == 0, "whole load instructions");
+#pragma unroll
+        for (int i = 0; i < KT * 20 / 256; ++i) {
+          const int sl = tid + 256 * i;
+          const int row = sl / 20, cp = sl - row * 20;
+          const int c = cp < 16 ? 4 * (cp >> 2) + ((cp & 3) ^ ((row >> 2) & 3)) : 0;
+          const uint32_t off = (uint32_t)(row * D + c * 8) * 2u;
+          lds_dma16_buf(ksrd, off, &lds_k[t & 1][(256 * i + wave * 64) * 8]);
+          lds_dma16_buf(vsrd, off, &lds_v[t & 1][(256 * i + wave * 64) * 8]);
+        }
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int c = tid + 256 * i;
@@ -422,13 +440,42 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   auto need_mask = [&](int n) {
     return (a.causal && n * 32 + 31 > q0_w) || n * 32 + 31 >= vlen || q0_w + 31 >= L;
   };
+  // K and V tile reads: at head_dim 128 one of four lane offsets plus an immediate (qg_additive)
+  int kro[2] = {0, 0}, kto[2] = {0, 0};
+  if constexpr (D == 128) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      kro[h] = qg_row_off(0, h, l32, g);
+      kto[h] = qg_tr_off(0, 0, h, g, l16, m16);
+    }
+  }
+  auto kv_row = [&](const unsigned short* tile, int sub, int kc) -> u32x4_t {
+    if constexpr (D == 128) return *(const u32x4_t*)(tile + kro[kc & 1] + sub * 32 * 160 + 32 * (kc >> 1));
+    else return frag_row<DP>(tile, sub * 32 + l32, 2 * kc + g);
+  };
+  auto kv_tr = [&](const unsigned short* tile, int sub, int kk, int fb) -> u32x4_t {
+    if constexpr (D == 128) {
+      u32x4_t f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const unsigned short* p = tile + kto[hh] + (sub * 32 + kk * 16) * 160 + 32 * fb;
+        const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+        const u32x2_t w = __builtin_bit_cast(u32x2_t, v);
+        f[2 * hh] = w[0];
+        f[2 * hh + 1] = w[1];
+      }
+      return f;
+    } else {
+      return frag_tr<DP>(tile, sub * 32 + kk * 16, fb, g, l16, m16);
+    }
+  };
+
   // one 32-key sub-tile n (sub within LDS tile tk / tv) in the rho^8 form E (two-branch) or not,
   // CLEAN (known live and unmasked: no tests, no selects) or guarded
   auto sub_tile = [&](const unsigned short* tk, const unsigned short* tv, int sub, int n, auto exact_tag,
                       auto clean_tag) {
     constexpr bool E = decltype(exact_tag)::value;
     constexpr bool CLEAN = decltype(clean_tag)::value;
-    const int rk = sub * 32 + l32;
     f32x16_t S, P;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -436,9 +483,9 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       P[e] = 0.f;
     }
 #pragma unroll
-    for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(frag_row<DP>(tk, rk, 2 * kc + g), qf[kc], S);
+    for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(kv_row(tk, sub, kc), qf[kc], S);
 #pragma unroll
-    for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(frag_row<DP>(tv, rk, 2 * kc + g), gf[kc], P);
+    for (int kc = 0; kc < NKC; ++kc) P = bmma<DT>(kv_row(tv, sub, kc), gf[kc], P);
     float ds[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -468,7 +515,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
     for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
-        dq[fb] = bmma<DT>(frag_tr<DP>(tk, sub * 32 + kk * 16, fb, g, l16, m16), dsp[kk], dq[fb]);
+        dq[fb] = bmma<DT>(kv_tr(tk, sub, kk, fb), dsp[kk], dq[fb]);
   };
   // The tile loops in one rho^8 form.  Tile t is clean when both its sub-tiles are the wave's and
   // need no mask; both tests only turn false as t grows, so the clean tiles are a prefix [0, tc)
