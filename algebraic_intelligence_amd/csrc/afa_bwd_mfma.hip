@@ -928,13 +928,35 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
             dsp[r4 >> 1][2 * (r4 & 1)] = Elem<DT>::pack(ds[0], ds[1]);
             dsp[r4 >> 1][2 * (r4 & 1) + 1] = Elem<DT>::pack(ds[2], ds[3]);
           }
+          if constexpr (NFB <= 4) {
+            // the transposed fragments of g, then of q, each batch read ahead of its MFMAs: one
+            // LDS round trip per batch instead of one per MFMA (the S and dP registers are free)
+            u32x4_t fr[NFB][2];
 #pragma unroll
-          for (int fb = 0; fb < NFB; ++fb)
+            for (int fb = 0; fb < NFB; ++fb)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-              dv[fb] = bmma<DT>(qg_tr(tg, sub, kk, fb), wp[kk], dv[fb]);
-              dk[fb] = bmma<DT>(qg_tr(tq, sub, kk, fb), dsp[kk], dk[fb]);
-            }
+              for (int kk = 0; kk < 2; ++kk) fr[fb][kk] = qg_tr(tg, sub, kk, fb);
+#pragma unroll
+            for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+              for (int kk = 0; kk < 2; ++kk) dv[fb] = bmma<DT>(fr[fb][kk], wp[kk], dv[fb]);
+#pragma unroll
+            for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+              for (int kk = 0; kk < 2; ++kk) fr[fb][kk] = qg_tr(tq, sub, kk, fb);
+#pragma unroll
+            for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+              for (int kk = 0; kk < 2; ++kk) dk[fb] = bmma<DT>(fr[fb][kk], dsp[kk], dk[fb]);
+          } else {
+#pragma unroll
+            for (int fb = 0; fb < NFB; ++fb)
+#pragma unroll
+              for (int kk = 0; kk < 2; ++kk) {
+                dv[fb] = bmma<DT>(qg_tr(tg, sub, kk, fb), wp[kk], dv[fb]);
+                dk[fb] = bmma<DT>(qg_tr(tq, sub, kk, fb), dsp[kk], dk[fb]);
+              }
+          }
         }
       }
       __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
