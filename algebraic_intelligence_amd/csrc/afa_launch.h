@@ -137,10 +137,10 @@ size_t f32_fwd_part_floats(const FwdArgs& a, int head_dim, int nsplit);
 hipError_t f32_fwd_launch(int head_dim, FwdArgs a, int nsplit, hipStream_t st);
 
 hipError_t generic_fwd_launch(int dtype, const GenArgs& a, hipStream_t st);
-// MFMA backward (afa_bwd_mfma.hip): bf16/fp16, head_dim 64 or 128, seq_len a multiple of 4,
-// contiguous tensors.  e_ws holds 2 * B*H*L floats (E, then 1/d).  With rotary tables (fp32,
-// 16-byte aligned) q and k are first rotated into rot_scratch (mfma_bwd_rot_bytes(a) bytes) and
-// dq, dk are rotated back in the store epilogues.
+// MFMA backward (afa_bwd_mfma.hip): bf16/fp16, head_dim 32, 48, 64, 96, 128 or 256, any seq_len,
+// contiguous tensors.  e_ws holds 2 * B*H*LP floats, LP = seq_len rounded up to 4 (-E, then
+// 1/d, per head).  With rotary tables (fp32, 16-byte aligned) q and k are first rotated into
+// rot_scratch (mfma_bwd_rot_bytes(a) bytes) and dq, dk are rotated back in the store epilogues.
 bool mfma_bwd_supported(int dtype, int head_dim, int64_t seq_len);
 size_t mfma_bwd_rot_bytes(const GenArgs& a);
 hipError_t mfma_bwd_launch(int dtype, const GenArgs& a, bool exact, void* rot_scratch, hipStream_t st);
