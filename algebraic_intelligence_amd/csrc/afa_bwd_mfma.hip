@@ -111,9 +111,8 @@ typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 constexpr int padded_dim(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
 // Layout of the dQ kernel's K and V tiles and of the dK/dV kernel's q and g tiles at head_dim 128:
-// each row is padded to 320 bytes
-// (20 chunk slots) and the chunks of each 64-byte group are XOR-swizzled by (r >> 2) & 3.  A row
-// starts 16 banks after the previous one, so the 4 rows of a transposed read's 32-lane pass fall
+// each row is padded to 320 bytes (20 chunk slots) and the chunks of each 64-byte group are
+// XOR-swizzled by (r >> 2) & 3.  A row starts 16 banks after the previous one, so the 4 rows of a transposed read's 32-lane pass fall
 // in 4 different 16-bank groups and the 16 rows of a row read's pass in 16 different 4-bank
 // quads (no conflicts).  The offsets of different 64-byte groups (fb, kc / 2) and of rows a
 // multiple of 16 apart differ by constants (qg_additive), so each read of a tile is one of four
@@ -647,7 +646,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       const i32x4_t qsrd = raw_buffer_srd_at(qp, (uint32_t)(L * D) * 2u, s0);
       const i32x4_t gsrd = raw_buffer_srd_at(gp, (uint32_t)(L * D) * 2u, s0);
       if constexpr (D == 128) {
-        // QT rows of 20 slots (qg_off): slot s = tid + 256 i holds chunk c of row s / 20; each
+        // QT rows of 20 slots (qg_off128): slot s = tid + 256 i holds chunk c of row s / 20; each
         // wave's instruction fills 64 consecutive slots, and the 4 padding slots of a row re-read
         // the row's first chunk (in bounds, never read back).  Waves whose slots all lie past the
         // tile skip the last instruction (every wait here is for all loads).
