@@ -1041,7 +1041,9 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
   // the fast-rho guard's query-block bounds go out first: they do not depend on k
   const float* qbm = !EXACT && a.qbm != nullptr ? a.qbm + (int64_t)bh * a.nkb : nullptr;
   const int qblk0 = t0 * QT / 64, qblk1 = (L + 63) / 64;
-  const float qbm_first = fast_rho_prefetch(qbm, qblk0, qblk1);
+  // (at head_dims padded to 64, whose 168 VGPRs are the three-wave limit, the bounds load after
+  // the k rows: a register held across the prologue costs a spill in the tile loop)
+  const float qbm_first = DP == 64 ? 0.f : fast_rho_prefetch(qbm, qblk0, qblk1);
 
   u32x4_t kf[NKC];
 #pragma unroll
@@ -1073,7 +1075,8 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
     float n2 = 0.0f;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) n2 += chunk_norm2<DT>(kf[kc]);
-    fast = fast_rho_safe(qbm, qblk0, qblk1, wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim, qbm_first);
+    fast = DP == 64 ? fast_rho_safe(qbm, qblk0, qblk1, wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim)
+                    : fast_rho_safe(qbm, qblk0, qblk1, wave_max(n2 + __shfl_xor(n2, 32)), a.nb_lim, qbm_first);
   }
   // head_dim 256 (one wave per SIMD, every accumulator in AGPRs, ~120 VGPRs spilled) takes the
   // two-branch form only: its instantiation holding both bodies returned wrong dv on the GPU
