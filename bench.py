@@ -46,7 +46,8 @@ VALU_LANE_OPS_PER_S = 16 * 1024 * 2.4e9
 WORKLOADS = {
     "c1": (1, 4, 256, 64, "fp32", False, None, False, "C1: AFA forward, fp32, non-causal (latency-bound)"),
     "c3": (8, 12, 4096, 64, "bf16", True, "c3", False,
-           "C3: AFA forward, causal, Cayley rotary fused in-kernel"),
+           "C3: AFA forward, causal, Cayley rotary inside the afa_fwd call (k rotated once by a pre-pass "
+           "kernel, q rotated at load by the attention kernel)"),
     "c2": (4, 8, 2048, 64, "bf16", True, None, False, "C2: AFA forward, causal"),
     "c4": (32, 4, 1024, 64, "bf16", True, "default", False,
            "C4: AFA forward, causal, default Cayley rotary"),
