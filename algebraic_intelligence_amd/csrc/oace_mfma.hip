@@ -4,11 +4,14 @@
 // logits z = h W, each with a fused epilogue, produce per-(vocabulary tile, row) partial sums:
 //   MODE_SQ:    sum_v z^2                                  -> tau = rsqrt(mean z^2 + eps)
 //   MODE_OCTIC: sum k8, sum rho7, sum (r x) k8, sum (r x) rho7 of x = tau z
-// which small kernels reduce in a fixed order into the row records; the row kernel also forms
-// the target logit h_n . W[:, t_n] (one d_model-long dot product per row) for rho and r x there.  The reference takes the
+// which small kernels reduce in a fixed order into the row records; the MODE_SQ epilogue also keeps
+// each row's target logit z[n][t_n], from which the row kernel forms rho and r x.  The reference takes the
 // second moment from the Gram matrix W W^T; the sum of squared logits is the same quantity and
 // a second sweep costs less than the Gram product whenever rows < d_model, the case of the
-// reference's own benchmark (512 x 768).  The backward recomputes z once:
+// reference's own benchmark (512 x 768).  When the fp32 logits fit the cache bound below, the
+// first sweep also stores them (MODE_SQZ) and one workgroup per row then forms tau, the octic
+// sums, the target's terms and the record from them in one pass (oace_mfma_row_cached_kernel),
+// in place of the second sweep.  The backward recomputes z once:
 //   MODE_DZ:    dz = tau c (r bracket - radial x), stored as the element type (rows, V padded)
 // and forms dh = dz W^T and dW = h^T dz with the MFMA GEMMs of oace_bwd_gemm.hip.
 //
@@ -53,6 +56,8 @@ struct GemmArgs {
   unsigned short* dz;  // MODE_DZ: (N, ldz)
   int64_t ldz;
   float* zc;  // MODE_SQZ: the fp32 logits, (N, ldz)
+  float* zt;  // MODE_SQ: the target logit of row n at zt[n * OACE_ROW] (the row record's unused last
+              // field until the row kernel finalises the record; not written for targets outside [0, V))
   float c0;
   const float* g_loss;
 };
@@ -122,6 +127,18 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[vb][nb][e] = 0.f;
+
+  // MODE_SQ keeps each row's target logit: the lane that will hold (row n, target) finds its
+  // element offset now, so the target loads complete under the main loop
+  int toff[4];
+  if constexpr (MODE == MODE_SQ) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int n = n0 + nb * 32 + l32;
+      const int64_t off = (n < a.N ? a.targets[n] : (int64_t)-1) - (v0 + wave * 64 + 4 * g);
+      toff[nb] = off >= 0 && off < 64 && (off & 4) == 0 ? (int)off : -1;
+    }
+  }
 
   const int T = a.d / KS;
   issue(0);
@@ -199,6 +216,18 @@ void oace_mfma_gemm_kernel(const GemmArgs a) {
           const int v = vw + 32 * vb + 8 * (e >> 2) + 4 * g + (e & 3);
           s[nb] += (!vtail || v < a.V) ? z * z : 0.f;
         }
+      if constexpr (MODE == MODE_SQ) {
+        // the target logit, for the row kernel (offset 32 vb + 8 (e >> 2) + (e & 3) in this lane)
+        if (toff[nb] >= 0) {
+          const int o = toff[nb], ovb = o >> 5, oe = ((o & 31) >> 3) * 4 + (o & 3);
+          float zt = 0.f;
+#pragma unroll
+          for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) zt = (vb == ovb && e == oe) ? acc[vb][nb][e] : zt;
+          a.zt[(int64_t)(n0 + nb * 32 + l32) * OACE_ROW] = zt;
+        }
+      }
       s[nb] += __shfl_xor(s[nb], 32);
       if (g == 0) red[wave * TN + nb * 32 + l32] = s[nb];
     }
@@ -308,28 +337,42 @@ __global__ __launch_bounds__(256) void oace_mfma_tau_kernel(const float* part, i
   if (lane == 0) rows[(int64_t)n * OACE_ROW + OACE_TAU] = o_rsq<float>(ss * inv_v + eps);
 }
 
-// The octic partial sums of the cached logits (the MODE_OCTIC epilogue's quantities): one wave
-// per (row, group of ZG vocabulary entries), 16 entries per lane read as f32x4, then one
-// reduction across the wave; partials [group][N][4] in the MODE_OCTIC layout.
-constexpr int ZG = 1024;
-__global__ __launch_bounds__(256) void oace_mfma_octic_cached_kernel(const float* zc, int64_t ldz, int N, int V,
-                                                                     int ngroups, const float* rows, float* part) {
-  const int lane = threadIdx.x & 63;
-  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (w >= (int64_t)N * ngroups) return;
-  const int n = (int)(w / ngroups), grp = (int)(w % ngroups);
-  const float tau = rows[(int64_t)n * OACE_ROW + OACE_TAU];
+// One row from the kept logits, in one workgroup: tau from the row's MODE_SQ partials (summed in
+// the order of oace_mfma_tau_kernel), the four octic sums over the row (16-byte loads, RC_UNROLL
+// of them in flight per lane while the previous group is evaluated), the target's rho and r x
+// from its own logit (the value the sums use), and the row record.  A target outside [0, V)
+// leaves rho_t = 0 (infinite loss), as the reference.
+constexpr int RC_THREADS = 512, RC_UNROLL = 4, RC_SPAN = 4 * RC_THREADS * RC_UNROLL;
+__global__ __launch_bounds__(RC_THREADS) void oace_mfma_row_cached_kernel(const float* part, int nvt, const float* zc,
+                                                                          int64_t ldz, int N, int V, float inv_v,
+                                                                          float eps, float gamma,
+                                                                          const int64_t* targets, float* rows) {
+  constexpr int NW = RC_THREADS / 64;
+  __shared__ float sh[NW * 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = blockIdx.x;
   const float* zrow = zc + (int64_t)n * ldz;
+  // Groups of RC_SPAN logits alternate between two register sets: the loads of the next group go
+  // out before the current one is evaluated.  Loads are unconditional (a lane past the padded row
+  // length reads the row's first entries, which are not used), so nothing waits on them early.
+  const int ld = (int)ldz;
+  auto load = [&](f32x4_t (&z)[RC_UNROLL], int v0) {
+#pragma unroll
+    for (int u = 0; u < RC_UNROLL; ++u) {
+      const int vs = v0 + 4 * (tid + RC_THREADS * u);
+      z[u] = *(const f32x4_t*)(zrow + (vs < ld ? vs : 0));
+    }
+  };
   float s[4] = {0.f, 0.f, 0.f, 0.f};
+  float tau;
+  auto eval = [&](const f32x4_t (&z)[RC_UNROLL], int v0) {
 #pragma unroll
-  for (int it = 0; it < ZG / 256; ++it) {
-    const int v0 = grp * ZG + it * 256 + 4 * lane;
-    if (v0 < V) {
-      const f32x4_t z4 = *(const f32x4_t*)(zrow + v0);
+    for (int u = 0; u < RC_UNROLL; ++u) {
+      const int vs = v0 + 4 * (tid + RC_THREADS * u);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (v0 + u < V) {
-          const float x = z4[u] * tau;
+      for (int e = 0; e < 4; ++e) {
+        if (vs + e < V) {
+          const float x = z[u][e] * tau;
           const Oct<float> o = octic_fast(x);
           const float rn = o.r * x;
           s[0] += o.k8;
@@ -339,15 +382,68 @@ __global__ __launch_bounds__(256) void oace_mfma_octic_cached_kernel(const float
         }
       }
     }
+  };
+  // Every wave sums the row's MODE_SQ partials itself, in the order of oace_mfma_tau_kernel (lane
+  // l adds partials l, l + 64, ...), so no barrier stands before the stream; the first chunk of
+  // partials is loaded before the first group of logits, whose loads stay in flight while it is
+  // added.
+  float ss = 0.f;
+  f32x4_t za[RC_UNROLL], zb[RC_UNROLL];
+  {
+    float p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = lane + 64 * u;
+      p[u] = part[(int64_t)(t < nvt ? t : 0) * N + n];
+    }
+    load(za, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ss += lane + 64 * u < nvt ? p[u] : 0.f;
+  }
+  for (int t0 = 256; t0 < nvt; t0 += 256) {
+    float p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + lane + 64 * u;
+      p[u] = t < nvt ? part[(int64_t)t * N + n] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ss += p[u];
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+  tau = o_rsq<float>(ss * inv_v + eps);
+  for (int v0 = 0; v0 < V; v0 += 2 * RC_SPAN) {
+    load(zb, v0 + RC_SPAN);
+    eval(za, v0);
+    load(za, v0 + 2 * RC_SPAN);
+    eval(zb, v0 + RC_SPAN);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) s[q] += __shfl_xor(s[q], m);
-  if (lane == 0) {
-    float* dst = part + ((int64_t)grp * N + n) * 4;
+    if (lane == 0) sh[wave * 4 + q] = s[q];
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float t4[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = s[q];
+    for (int q = 0; q < 4; ++q) {
+      float x = 0.f;
+      for (int w = 0; w < NW; ++w) x += sh[w * 4 + q];
+      t4[q] = x;
+    }
+    const int64_t t = targets[n];
+    float rho_t = 0.f, rn_t = 0.f;
+    if (t >= 0 && t < V) {
+      const float x = zrow[t] * tau;
+      const Oct<float> o = octic(x);
+      rho_t = o.rho;
+      rn_t = o.r * x;
+    }
+    oace_finalize_row<float>(rows + (int64_t)n * OACE_ROW, tau, t4[0], t4[1], t4[2], t4[3], rho_t, rn_t, inv_v,
+                             gamma);
   }
 }
 
@@ -402,30 +498,16 @@ __global__ __launch_bounds__(256) void oace_mfma_dz_cached_kernel(const float* z
   }
 }
 
-// Row records from the MODE_OCTIC partials, one wave per row.  The target logit is the dot
-// product of the row of h with row t of W^T (fp32 accumulation of the exact element products,
-// as the GEMM); a target outside [0, V) leaves rho_t = 0 (infinite loss), as the reference.
-template <int DT>
+// Row records from the MODE_OCTIC partials, one wave per row.  The target logit is the one the
+// MODE_SQ sweep kept in the record's last field (the GEMM's own value, as the sums use); a target
+// outside [0, V) leaves rho_t = 0 (infinite loss), as the reference.
 __global__ __launch_bounds__(256) void oace_mfma_rows_kernel(const float* part, int nvt, int N, float inv_v,
-                                                             float gamma, const unsigned short* h, int64_t ldh,
-                                                             const unsigned short* wt, int64_t ldwt, int d, int V,
-                                                             const int64_t* targets, float* rows) {
+                                                             float gamma, int V, const int64_t* targets, float* rows) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int64_t t = targets[n];
   const bool valid = t >= 0 && t < V;
-  float z = 0.f;
-  if (valid) {
-    const unsigned short* hr = h + (int64_t)n * ldh;
-    const unsigned short* wr = wt + t * ldwt;
-    for (int k = 2 * lane; k < d; k += 128) {
-      const unsigned hw = *(const unsigned*)(hr + k), ww = *(const unsigned*)(wr + k);
-      z += Elem<DT>::lo(hw) * Elem<DT>::lo(ww) + Elem<DT>::hi(hw) * Elem<DT>::hi(ww);
-    }
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) z += __shfl_xor(z, m);
   float s[4] = {0.f, 0.f, 0.f, 0.f};
   for (int vt = lane; vt < nvt; vt += 64)
 #pragma unroll
@@ -439,7 +521,7 @@ __global__ __launch_bounds__(256) void oace_mfma_rows_kernel(const float* part, 
     const float tau = rec[OACE_TAU];
     float rho_t = 0.f, rn_t = 0.f;
     if (valid) {
-      const float x = z * tau;
+      const float x = rec[OACE_ROW - 1] * tau;
       const Oct<float> o = octic(x);
       rho_t = o.rho;
       rn_t = o.r * x;
@@ -566,31 +648,25 @@ hipError_t oace_linear_fwd_mfma(int dtype, const OaceArgs& a, void* rows, void* 
     g.ldz = ldz_of(a.V);
     e = launch_gemm_dt<MODE_SQZ>(dtype, g, st);
   } else {
+    g.zt = (float*)rows + (OACE_ROW - 1);
     e = launch_gemm_dt<MODE_SQ>(dtype, g, st);
   }
   if (e != hipSuccess) return e;
+  if (zc) {
+    hipLaunchKernelGGL(oace_mfma_row_cached_kernel, dim3((unsigned)a.N), dim3(RC_THREADS), 0, st, (const float*)part,
+                       g.nvt, (const float*)g.zc, g.ldz, g.N, g.V, inv_v, (float)a.eps, (float)a.gamma, a.targets,
+                       (float*)rows);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    return oace_mean_launch(dtype, rows, a.N, a.loss, st);
+  }
   const unsigned rg = (unsigned)((a.N + 3) / 4);
   hipLaunchKernelGGL(oace_mfma_tau_kernel, dim3(rg), dim3(256), 0, st, (const float*)part, g.nvt, g.N, inv_v,
                      (float)a.eps, (float*)rows);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  int nparts = g.nvt;  // partial sums per row for the row kernel
-  if (zc) {
-    nparts = (int)((a.V + ZG - 1) / ZG);
-    const unsigned og = (unsigned)(((int64_t)a.N * nparts + 3) / 4);
-    hipLaunchKernelGGL(oace_mfma_octic_cached_kernel, dim3(og), dim3(256), 0, st, (const float*)g.zc, g.ldz, g.N,
-                       g.V, nparts, (const float*)rows, part);
-    e = hipGetLastError();
-  } else {
-    e = launch_gemm_dt<MODE_OCTIC>(dtype, g, st);
-  }
-  if (e != hipSuccess) return e;
+  if ((e = launch_gemm_dt<MODE_OCTIC>(dtype, g, st)) != hipSuccess) return e;
   const unsigned wg = (unsigned)((a.N + 3) / 4);
-  if (dtype == AFA_BF16)
-    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_BF16>, dim3(wg), dim3(256), 0, st, (const float*)part, nparts, g.N,
-                       inv_v, (float)a.gamma, g.h, g.ldh, wt, ldwt, g.d, g.V, a.targets, (float*)rows);
-  else
-    hipLaunchKernelGGL(oace_mfma_rows_kernel<AFA_F16>, dim3(wg), dim3(256), 0, st, (const float*)part, nparts, g.N,
-                       inv_v, (float)a.gamma, g.h, g.ldh, wt, ldwt, g.d, g.V, a.targets, (float*)rows);
+  hipLaunchKernelGGL(oace_mfma_rows_kernel, dim3(wg), dim3(256), 0, st, (const float*)part, g.nvt, g.N, inv_v,
+                     (float)a.gamma, g.V, a.targets, (float*)rows);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return oace_mean_launch(dtype, rows, a.N, a.loss, st);
 }

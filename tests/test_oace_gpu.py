@@ -164,7 +164,8 @@ def test_kept_logits_match_recomputed(shape, dtype, tied):
     """The forward that keeps the fp32 logits (octic sums from them) against the two-sweep forward
     (OACE_FLAG_RECOMPUTE_Z): the same sums in another order.  On one forward's row records, the
     backward's dz from the kept logits (OACE_FLAG_Z_READY) against the dz GEMM sweep: the same
-    fp32 logits and arithmetic, so dh and dW are bitwise equal."""
+    fp32 logits and arithmetic, so dh and dW are bitwise equal.  The gradients from the two
+    forwards' records agree to one rounding of the element type."""
     N, d, V = shape
     h, w, t = _case(N, d, V, dtype, seed=N + 2 * d + V, scale=1.0 if dtype == torch.bfloat16 else 0.5)
     if tied:
@@ -178,7 +179,13 @@ def test_kept_logits_match_recomputed(shape, dtype, tied):
     gh, gw = _grads(stale_h, 1.0)
     assert torch.equal(dh, gh) and torch.equal(dw, gw)
     rh, rw = _grads(rcache, 1.0)
-    assert normwise(to_f64(dh), to_f64(rh)) <= 1e-3 and normwise(to_f64(dw), to_f64(rw)) <= 1e-3
+    # the two records differ in the order of their fp32 sums, so an output that sits at a rounding
+    # boundary of the element type can round the other way: at most one unit in the last place of
+    # the largest element (the element type's eps), and in few elements
+    ulp = torch.finfo(dtype).eps
+    for x, y in ((dh, rh), (dw, rw)):
+        assert normwise(to_f64(x), to_f64(y)) <= ulp
+        assert (x != y).double().mean().item() <= 1e-2
 
 
 def test_backward_after_inputs_change_in_place():
