@@ -82,6 +82,33 @@ OACE_WORKLOADS = {
 }
 
 
+def environment():
+    """What the line was measured with, after the reference's evidence records (which carry
+    package versions and the sha256 of every source file, scripts/phase6_records.py:23-50):
+    the GPU and its ISA, the HIP and torch versions, the sha256 (first 16 hex digits) of the loaded
+    libafa_hip.so and of the kernel sources it was built from, and the host's CPU count."""
+    import glob
+    import hashlib
+
+    import torch
+
+    from algebraic_intelligence_amd import _lib
+
+    def sha(paths):
+        h = hashlib.sha256()
+        for p in paths:
+            with open(p, "rb") as f:
+                h.update(os.path.basename(p).encode() + b"\0" + f.read())
+        return h.hexdigest()[:16]
+
+    props = torch.cuda.get_device_properties(0)
+    srcs = sorted(glob.glob(os.path.join(ROOT, "algebraic_intelligence_amd", "csrc", "*")))
+    return {"gpu": props.name, "arch": getattr(props, "gcnArchName", None),
+            "compute_units": props.multi_processor_count, "hip": torch.version.hip,
+            "torch": torch.__version__, "lib_sha16": sha([_lib.LIB_PATH]), "csrc_sha16": sha(srcs),
+            "host_cpus": len(os.sched_getaffinity(0))}
+
+
 def warm_up(step, args):
     """args.warmup untimed steps, then more until args.warmup_seconds have passed, so the timed
     steps run at the clock the GPU holds under sustained load.  Returns (steps run, seconds)."""
@@ -744,6 +771,7 @@ def main():
     if not args.no_cpu and args.workload == "c3":
         line["cpu_baseline"] = cpu_baseline(q, k, v, rot, args.cpu_seconds)
         line["cpu_baseline"]["gpu_speedup"] = round(tflops / line["cpu_baseline"]["value"], 1)
+    line["environment"] = environment()
     print(json.dumps(line), flush=True)
 
 
