@@ -9,7 +9,9 @@
 // hipGetSymbolAddress gives the copy's address, which is kept per device and passed to afa_fwd.
 // Nothing in the workspace has to start at zero: every region afa_fwd uses (the rotated k, the
 // fast-rho key bounds, the fp32 split-K partials) is written in full by the call before it is
-// read.  All calls on one device share its array, so calls that overlap on one device (on
+// read, and the key split's per-block counters, which do count from zero, are cleared by a kernel
+// of the same call (the norm or K-rotation pre-pass) before the attention kernel runs.  All calls
+// on one device share its array, so calls that overlap on one device (on
 // different streams, or from several threads without ordering) race; calls ordered on one
 // stream do not.
 #include <mutex>
