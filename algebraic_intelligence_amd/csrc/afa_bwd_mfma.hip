@@ -20,7 +20,7 @@
 // reads return exactly those rows for the A operand.
 //
 // Tiles of 64 rows are loaded by direct global -> LDS loads into two buffers; rows are D
-// elements with 16-byte chunks XOR-swizzled by (row & 7) (conflict-free 32-row fragments).
+// elements with 16-byte chunks XOR-swizzled by a key of the row (swz_key: conflict-free fragments).
 // 1/sqrt(D) is split into 1/8 folded into the register-resident operand (exact) and the factor
 // 8 fl(1/sqrt D) applied to the fp32 score (the same rounding as s * scale; 1 at D = 64); at
 // head_dim 128 in bf16, 1/16 is folded and the score factor sqrt 2 enters the rho^8 formula
@@ -61,23 +61,38 @@ __device__ __forceinline__ u32x4_t bscale(u32x4_t w, float sc) {
   return r;
 }
 
-// XOR key of row r's 16-byte chunks in a swizzled tile of D-element rows: chunk c of row r sits
-// at position c ^ key.  At D = 128 (256-byte rows, one full period of the LDS banks) the key
-// takes all 16 values over 16 rows, so a row fragment read (32 rows, one chunk each) uses every
-// bank, and it sends the 8 rows of a transposed read (4 consecutive chunks each) to 4 different
-// 4-chunk groups, two rows each; at D = 64 two rows share a bank period and r & 7 does both.
+constexpr int padded_dim(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
+
+// XOR key of row r's 16-byte chunks in a swizzled tile of rows of padded_dim(D) elements: chunk c
+// of row r sits at position c ^ key.  With 128-element rows (256 bytes, one full period of the LDS
+// banks) the key takes all 16 values over 16 rows, so a row fragment read (32 rows, one chunk
+// each) uses every bank, and it sends the 8 rows of a transposed read (4 consecutive chunks each)
+// to 4 different 4-chunk groups, two rows each.  With 64-element rows (128 bytes) an even and an
+// odd row share a bank period, so the 16 rows of a row read's pass (16 lanes x 16 bytes) fill the
+// 16 slots of a period when the key takes all 8 values over the even rows and over the odd rows,
+// and the 4 rows of a transposed read's pass (32 lanes x 8 bytes: 4 consecutive chunks of each
+// row) do when rows r and r + 2 of an aligned group of 4 differ in bit 2 of the key:
+// key(r) = f(r >> 1) with f(i) = 4 (i & 1) + ((i >> 1) & 3).  r & 7 meets the first condition for
+// 8 rows only and not the second: rocprofv3 counted 2-way conflicts, 81 and 48 cycles per
+// 1024-score unit in dK/dV and dQ at head_dim 64 (C3 backward 532 -> 538 TFLOP/s without them).
+// Head dims padded to 64 (32, 48) keep r & 7: there the new key's offsets made the dK/dV kernel
+// spill at its three-wave register limit (head_dim 48 3% slower).
+__host__ __device__ constexpr int swz_key_of(int D, int r) {
+  return padded_dim(D) == 128 ? ((r & 15) ^ ((r & 3) << 2)) : D == 64 ? (((r & 2) << 1) | ((r >> 2) & 3)) : (r & 7);
+}
 template <int D>
 __device__ __forceinline__ int swz_key(int r) {
-  if constexpr (D == 128) return (r & 15) ^ ((r & 3) << 2);
-  else return r & 7;
+  return swz_key_of(D, r);
 }
 
-// Element offset of 16-byte chunk `c` of row `r` in a swizzled tile of D-element rows.
+// Element offset of 16-byte chunk `c` of row `r` in a swizzled tile (D: the head dim, rows of
+// padded_dim(D) elements).
 template <int D>
 __device__ __forceinline__ int swz(int r, int c) {
-  if constexpr (D == 128) return r * D + ((c ^ swz_key<D>(r)) << 3);
+  constexpr int DP = padded_dim(D);
+  if constexpr (DP == 128) return r * DP + ((c ^ swz_key<D>(r)) << 3);
   // (c & ~7) is a compile-time constant at every call, so chunks 8 apart share one lane offset
-  else return r * D + ((((c & 7) ^ (r & 7)) | (c & ~7)) << 3);
+  else return r * DP + ((((c & 7) ^ swz_key<D>(r)) | (c & ~7)) << 3);
 }
 
 // Row fragment: 8 elements (chunk c) of row r.
@@ -108,7 +123,6 @@ __device__ __forceinline__ u32x4_t frag_tr(const unsigned short* tile, int r0, i
 
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
-constexpr int padded_dim(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
 // Layout of the dQ kernel's K and V tiles and of the dK/dV kernel's q and g tiles at head_dim 128:
 // each row is padded to 320 bytes (20 chunk slots) and the chunks of each 64-byte group are
@@ -403,7 +417,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       for (int i = 0; i < CPT; ++i) {
         const int c = tid + 256 * i;
         const int row = c / NCK, pc = c % NCK;
-        const int lc = pc ^ swz_key<DP>(row);
+        const int lc = pc ^ swz_key<D>(row);
         const uint32_t off = (uint32_t)(row * D + lc * 8) * 2u;
         lds_dma16_buf(ksrd, off, &lds_k[t & 1][(256 * i + wave * 64) * 8]);
         lds_dma16_buf(vsrd, off, &lds_v[t & 1][(256 * i + wave * 64) * 8]);
@@ -415,7 +429,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       const int c = tid + 256 * i;               // LDS chunk slot
       const int row = c / NCK, pc = c % NCK;
       const int key = min(t * KT + row, L - 1);
-      const int lc = pc ^ swz_key<DP>(row);
+      const int lc = pc ^ swz_key<D>(row);
       unsigned short* kd = &lds_k[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* vd = &lds_v[t & 1][(256 * i + wave * 64) * 8];
       // byte offset within the head (L * D < 2^31, mfma_bwd_supported): a uniform base plus a
@@ -450,7 +464,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
   }
   auto kv_row = [&](const unsigned short* tile, int sub, int kc) -> u32x4_t {
     if constexpr (D == 128) return *(const u32x4_t*)(tile + kro[kc & 1] + sub * 32 * 160 + 32 * (kc >> 1));
-    else return frag_row<DP>(tile, sub * 32 + l32, 2 * kc + g);
+    else return frag_row<D>(tile, sub * 32 + l32, 2 * kc + g);
   };
   auto kv_tr = [&](const unsigned short* tile, int sub, int kk, int fb) -> u32x4_t {
     if constexpr (D == 128) {
@@ -465,7 +479,7 @@ void afa_bwd_mfma_dq_kernel(const GenArgs a) {
       }
       return f;
     } else {
-      return frag_tr<DP>(tile, sub * 32 + kk * 16, fb, g, l16, m16);
+      return frag_tr<D>(tile, sub * 32 + kk * 16, fb, g, l16, m16);
     }
   };
 
@@ -667,7 +681,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       for (int i = 0; i < CPT; ++i) {
         const int c = tid + 256 * i;
         const int row = c / NCK, pc = c % NCK;
-        const int lc = pc ^ swz_key<DP>(row);
+        const int lc = pc ^ swz_key<D>(row);
         const uint32_t off = (uint32_t)(row * D + lc * 8) * 2u;
         lds_dma16_buf(qsrd, off, &lds_q[t & 1][(256 * i + wave * 64) * 8]);
         lds_dma16_buf(gsrd, off, &lds_g[t & 1][(256 * i + wave * 64) * 8]);
@@ -679,7 +693,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       const int c = tid + 256 * i;
       const int row = c / NCK, pc = c % NCK;
       const int qrow = min(t * QT + row, L - 1);
-      const int lc = pc ^ swz_key<DP>(row);
+      const int lc = pc ^ swz_key<D>(row);
       unsigned short* qd = &lds_q[t & 1][(256 * i + wave * 64) * 8];
       unsigned short* gd = &lds_g[t & 1][(256 * i + wave * 64) * 8];
       const uint32_t off = (uint32_t)(qrow * D + lc * 8) * 2u;
@@ -713,7 +727,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
   }
   auto qg_row = [&](const unsigned short* tile, int sub, int kc) -> u32x4_t {
     if constexpr (D == 128) return *(const u32x4_t*)(tile + qro[kc & 1] + sub * 32 * 160 + 32 * (kc >> 1));
-    else return frag_row<DP>(tile, sub * 32 + l32, 2 * kc + g);
+    else return frag_row<D>(tile, sub * 32 + l32, 2 * kc + g);
   };
   auto qg_tr = [&](const unsigned short* tile, int sub, int kk, int fb) -> u32x4_t {
     if constexpr (D == 128) {
@@ -728,7 +742,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
       }
       return f;
     } else {
-      return frag_tr<DP>(tile, sub * 32 + kk * 16, fb, g, l16, m16);
+      return frag_tr<D>(tile, sub * 32 + kk * 16, fb, g, l16, m16);
     }
   };
 
@@ -768,7 +782,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(qg_row(tq, sub, kc), kf[kc], S);
 #pragma unroll
           for (int kc = 0; kc < NKC; ++kc) {
-            const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
+            const u32x4_t vk = frag_row<D>(lds_vk, wave * 32 + l32, 2 * kc + g);
             P = bmma<DT>(qg_row(tg, sub, kc), vk, P);
           }
           // W and dS, masked and packed to the element type four rows at a time (only those four
@@ -883,7 +897,7 @@ __device__ __forceinline__ void dkdv_body(const GenArgs& a, DkdvLds<padded_dim(D
           for (int kc = 0; kc < NKC; ++kc) S = bmma<DT>(qg_row(tq, sub, kc), kf[kc], S);
 #pragma unroll
           for (int kc = 0; kc < NKC; ++kc) {
-            const u32x4_t vk = frag_row<DP>(lds_vk, wave * 32 + l32, 2 * kc + g);
+            const u32x4_t vk = frag_row<D>(lds_vk, wave * 32 + l32, 2 * kc + g);
             P = bmma<DT>(qg_row(tg, sub, kc), vk, P);
           }
           // W and dS, masked and packed to the element type four rows at a time (only those four
@@ -1061,7 +1075,7 @@ void afa_bwd_mfma_dkdv_kernel(const GenArgs a) {
       const int c = tid + 256 * i;
       const int row = c / NCK, pc = c % NCK;
       const int key = min(k0_wg + row, L - 1);
-      const int lc = pc ^ swz_key<DP>(row);
+      const int lc = pc ^ swz_key<D>(row);
       const void* vs = (const void*)((const char*)vp + (uint32_t)(key * D + lc * 8) * 2u);
       if constexpr (D < DP) {
         if (lc >= D / 8) vs = (const void*)afa_bwd_zero_chunk;
