@@ -6,9 +6,12 @@
 //   ds = 8 scale r w (g_i . v_j - E_i);  dq_i += ds_ij k_j;  dk_j += ds_ij q_i;  dv_j += w_ij g_i,
 // with ds and w rounded to the input dtype as MFMA operands and fp32 accumulation.
 //
-// Three launches (four with rotary tables), no atomics:
-//   * afa_bwd_mfma_rotate_kernel (rotary tables only): q and k rotated once into scratch; dq and
-//     dk are rotated back through R^T in the dQ / dK store epilogues;
+// Three launches after the pre-passes of q and k (rotation with rotary tables, the fast-rho
+// guard's block bounds), no atomics:
+//   * rotary tables only: q and k rotated once into scratch by the forward's K rotation pass
+//     (afa_krot_kernel, which also writes the fast-rho guard's block bounds of the rotated rows),
+//     or by afa_bwd_mfma_rotate_kernel where no bounds are needed or at head_dim 256; dq and dk
+//     are rotated back through R^T in the dQ / dK store epilogues;
 //   * afa_bwd_mfma_prep_kernel: -E_i and 1/d_i per row into the workspace;
 //   * afa_bwd_mfma_dq_kernel (one lane per query, like the forward): S^T = K Q^T, dP^T = V g^T on
 //     MFMA, W and dS on the VALU, dQ^T += K^T dS^T with K^T read from the same LDS tile by
@@ -1118,21 +1121,50 @@ size_t mfma_bwd_rot_bytes(const GenArgs& a) { return (size_t)a.B * a.H * a.L * a
 template <int DT, int D, bool EXACT>
 static hipError_t bwd_launch(GenArgs a, void* rot_scratch, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.H * a.L;
+  const bool guard = !EXACT && a.qbm != nullptr && a.kbm != nullptr;
+  const int64_t sl = a.D, sh = (int64_t)a.L * a.D, sb = (int64_t)a.H * sh;  // q, k: contiguous
+  bool bounded = false;  // the guard's bounds already written by the rotation
   if (a.rc != nullptr) {
     if (rot_scratch == nullptr) return hipErrorInvalidValue;
     unsigned short* qr = (unsigned short*)rot_scratch;
     unsigned short* kr = qr + rows * D;
-    const int64_t chunks = rows * (D / 8);
-    const unsigned gx = (unsigned)std::min<int64_t>((chunks + 255) / 256, 4096);
-    hipLaunchKernelGGL((afa_bwd_mfma_rotate_kernel<DT, D>), dim3(gx, 2), dim3(256), 0, st, a, qr, kr);
+    if (guard && D <= 128) {
+      // the forward's K rotation pass (afa_krot_kernel), once for q and once for k: the same fp32
+      // rotation and rounding as afa_bwd_mfma_rotate_kernel, and each 64-row block's largest
+      // squared norm from the rotated rows as they are written, in place of a second pass
+      FwdArgs f = {};
+      f.B = a.B;
+      f.H = a.H;
+      f.L = a.L;
+      f.rc = (const float*)a.rc;
+      f.rs = (const float*)a.rs;
+      f.k = a.q;
+      f.k_b = sb;
+      f.k_h = sh;
+      f.k_l = sl;
+      hipError_t e = krot_launch(DT, D, f, qr, (float*)a.qbm, st);
+      f.k = a.k;
+      f.k_b = sb;
+      f.k_h = sh;
+      f.k_l = sl;
+      if (e == hipSuccess) e = krot_launch(DT, D, f, kr, (float*)a.kbm, st);
+      if (e != hipSuccess) return e;
+      bounded = true;
+    } else {
+      const int64_t chunks = rows * (D / 8);
+      const unsigned gx = (unsigned)std::min<int64_t>((chunks + 255) / 256, 4096);
+      hipLaunchKernelGGL((afa_bwd_mfma_rotate_kernel<DT, D>), dim3(gx, 2), dim3(256), 0, st, a, qr, kr);
+    }
     a.q = qr;
     a.k = kr;
   }
-  if (!EXACT && a.qbm != nullptr && a.kbm != nullptr) {
+  if (guard) {
     // fast-rho guard bounds of the (rotated) q and k rows; without them every tile is exact
-    const int64_t sl = a.D, sh = (int64_t)a.L * a.D, sb = (int64_t)a.H * sh;
-    hipError_t e = rownorm_launch(DT, a.q, sb, sh, sl, a.B, a.H, a.L, a.D, (float*)a.qbm, st);
-    if (e == hipSuccess) e = rownorm_launch(DT, a.k, sb, sh, sl, a.B, a.H, a.L, a.D, (float*)a.kbm, st);
+    hipError_t e = hipSuccess;
+    if (!bounded) {
+      e = rownorm_launch(DT, a.q, sb, sh, sl, a.B, a.H, a.L, a.D, (float*)a.qbm, st);
+      if (e == hipSuccess) e = rownorm_launch(DT, a.k, sb, sh, sl, a.B, a.H, a.L, a.D, (float*)a.kbm, st);
+    }
     if (e != hipSuccess) return e;
     a.nkb = (a.L + 63) / 64;
     // dQ forms s = S * score_factor with q / 8 and k as stored (dK/dV: q and k / 8); the half

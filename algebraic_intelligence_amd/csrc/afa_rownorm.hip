@@ -4,8 +4,8 @@
 // sum_d x_ld^2 in fp32 from the bf16 / fp16 elements as stored.  The MFMA kernels bound every
 // score of a key tile by Cauchy-Schwarz with it (|q . k| <= |q| |k|) and use the branch-free
 // rho^8 only where that bound keeps |s| <= kFastRhoMaxScore.  It reads the tensor once and writes
-// B H ceil(L/64) floats; with rotary tables the rotation pre-passes produce the same bounds from
-// the rotated rows instead (afa_krot_kernel, afa_bwd_mfma_rotate_kernel).
+// B H ceil(L/64) floats; with rotary tables the K rotation pass (afa_krot_kernel) produces the
+// same bounds from the rotated rows instead, for the forward's k and the backward's q and k.
 #include <cmath>
 
 #include "afa_common.h"
