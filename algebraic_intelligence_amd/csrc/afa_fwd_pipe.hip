@@ -10,10 +10,10 @@
 //     around their own MFMAs and S alternates between two register sets, which keeps a wave at
 //     <= 256 VGPRs (D = 128: two waves per SIMD) or <= 168 (D = 64: three waves per SIMD);
 //   * K and V reach LDS by direct global -> LDS loads in tiles of 32 keys (rows of D/8 16-byte
-//     chunks): K chunk c of row r at c ^ (r & 7) (conflict-free 32-row fragments); V chunk c at
-//     c ^ ((r & 3) << 1) for D = 128 and c ^ (((r >> 1) & 1) << 2) for D = 64 (conflict-free
-//     ds_read_tr16_b64 of 4-key column slices, which give the PV MFMA's A operand in the key
-//     order of the S^T accumulator);
+//     chunks): K chunk c of row r at c ^ k_key(r) (r & 15 for D = 128, (r >> 1) & 7 for D = 64:
+//     conflict-free fragment reads); V chunk c at c ^ ((r & 3) << 2) for D = 128 and
+//     c ^ (((r >> 1) & 1) << 2) for D = 64 (conflict-free ds_read_tr16_b64 of 4-key column
+//     slices, which give the PV MFMA's A operand in the key order of the S^T accumulator);
 //   * LDS is a ring of NB tiles: iteration u issues tile u + NB - 1 into the buffer of tile u - 1
 //     and waits only for its own loads of tile u + 1; one barrier per tile;
 //   * q is scaled by 1/sqrt(D) (and Cayley-rotated in fp32 when rotary tables are given) as it is
@@ -88,6 +88,16 @@ __device__ __forceinline__ float tree16x(const float (&p)[16]) {
   return a[0] + a[2];
 }
 
+// K chunk c of tile row r sits at c ^ k_key(r).  At DP = 128 a 256-byte row is one bank period and
+// r & 15 spreads the 16 rows of a fragment read's pass (16 lanes x 16 bytes) over its 16 slots; at
+// DP = 64 an even and an odd row share a period, and (r >> 1) & 7 takes all 8 positions over the
+// even rows and over the odd ones (r & 7 took them over 8 rows only: 2-way conflicts).
+template <int DP>
+__device__ __forceinline__ int k_key(int r) {
+  if constexpr (DP == 128) return r & 15;
+  else return (r >> 1) & 7;
+}
+
 template <int D>
 __device__ __forceinline__ int v_swizzle(int r, int c) {
   if constexpr (D == 128) return c ^ ((r & 3) << 2);
@@ -158,7 +168,7 @@ using PipeTile = unsigned short[32 * DP];
 
 // Direct global -> LDS loads of key tile t (32 keys of K and of V) of one head into ring buffer
 // buf = t % NB: slot s = tid + 256 i covers row s / CH, physical chunk s % CH; K chunk c of row r goes to
-// c ^ (r mod CH) (every chunk position of the row in turn), V chunk c to v_swizzle; rows past L
+// c ^ k_key(r), V chunk c to v_swizzle; rows past L
 // read zeros (buffer loads whose range ends with row L - 1) or, at head dims with padding
 // chunks, row L - 1: finite data for masked keys.
 template <int D>
@@ -186,7 +196,7 @@ __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padde
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int s = tid + 256 * i, r = s / CH, pc = s % CH;
-      const int lk = pc ^ (r & (CH - 1)), lv = v_swizzle<DP>(r, pc);
+      const int lk = pc ^ k_key<DP>(r), lv = v_swizzle<DP>(r, pc);
       lds_dma16_buf(ksrd, (uint32_t)(r * (int)a.k_l + lk * 8) * 2u, kd + (256 * i + wave * 64) * 8);
       lds_dma16_buf(vsrd, (uint32_t)(r * (int)a.v_l + lv * 8) * 2u, vd + (256 * i + wave * 64) * 8);
     }
@@ -196,7 +206,7 @@ __device__ __forceinline__ void pipe_issue_tile(const FwdArgs& a, PipeTile<padde
   for (int i = 0; i < LPT; ++i) {
     const int s = tid + 256 * i, r = s / CH, pc = s % CH;
     const int key = min(t * KT + r, a.L - 1);
-    const int lk = pc ^ (r & (CH - 1)), lv = v_swizzle<DP>(r, pc);
+    const int lk = pc ^ k_key<DP>(r), lv = v_swizzle<DP>(r, pc);
     // byte offsets within the head fit 32 bits (checked by the caller): a uniform base plus a
     // 32-bit lane offset per load
     const void* ks = (const void*)((const char*)kp + (uint32_t)(key * (int)a.k_l + lk * 8) * 2u);
@@ -253,7 +263,7 @@ __device__ __forceinline__ void pipe_body(const FwdArgs& a, PipeTile<padded_dim(
   auto read_kf = [&](int buf) {
     const unsigned short* base = &lds_k[buf][l32 * DP];
 #pragma unroll
-    for (int kc = 0; kc < NK; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ (l32 & (CH - 1))) * 8));
+    for (int kc = 0; kc < NK; ++kc) kf[kc] = *(const u32x4_t*)(base + (((2 * kc + g) ^ k_key<DP>(l32)) * 8));
   };
   auto read_vf = [&](int buf) {
     const unsigned short* tile = lds_v[buf];
