@@ -239,6 +239,55 @@ def rotate_tensor(x: torch.Tensor, c: torch.Tensor, s: torch.Tensor, seq_axis: i
     return _Rotate.apply(_float_input(x), c, s, seq_axis % x.ndim)
 
 
+def _align_param(param, q_shape, seq_axis=None):
+    """The first seq_len rows of a (positions, D/2) table, shaped to broadcast against the
+    (..., D/2) feature pairs of a q_shape tensor: size seq_len on the sequence axis, D/2 last, 1
+    elsewhere (src/attention.py:123-139; the model aligns its tables this way before
+    _rotate_tensor, src/model.py:355-357).  A view of param, no copy."""
+    q_shape = tuple(q_shape)
+    ndim = len(q_shape)
+    if seq_axis is None:
+        seq_axis = _infer_seq_axis(q_shape, param.shape[0])
+    seq_len = q_shape[seq_axis]
+    shape = [1] * (ndim - 1) + [q_shape[-1] // 2]
+    shape[seq_axis] = seq_len
+    return param[:seq_len].reshape(shape)
+
+
+def _rotate_tensor(x, c, s):
+    """Rotate (even, odd) feature pairs of x by tables that broadcast against its (..., D/2)
+    pairs (src/attention.py:142-152), as the model calls it on (B, H, T, D) q and k with tables
+    from _align_param (src/model.py:263-264).  The tables may vary along one leading axis, the
+    sequence axis, and are cast to x's dtype before the rotation, as the reference casts them.
+    Runs ago_rotate; differentiable with respect to x."""
+    x = _float_input(x)
+    if x.ndim < 1 or x.shape[-1] % 2 != 0:
+        raise ValueError(f"Feature dimension must be even, got {tuple(x.shape)}")
+    pairs = x.shape[-1] // 2
+    c = torch.as_tensor(c, device=x.device)
+    s = torch.as_tensor(s, device=x.device)
+    if c.shape != s.shape or c.ndim < 1 or c.ndim > x.ndim or c.shape[-1] != pairs:
+        raise ValueError(f"rotary tables of shapes {tuple(c.shape)} and {tuple(s.shape)} do not broadcast "
+                         f"against the feature pairs of {tuple(x.shape)}")
+    lead = (1,) * (x.ndim - c.ndim) + tuple(c.shape[:-1])
+    axes = [ax for ax, n in enumerate(lead) if n != 1]
+    if len(axes) > 1 or any(n != 1 and n != x.shape[ax] for ax, n in enumerate(lead)):
+        raise ValueError(f"rotary tables of shape {tuple(c.shape)} must vary along at most one axis of "
+                         f"{tuple(x.shape)}, its sequence axis")
+    if axes:
+        seq_axis = axes[0]
+        rows_c, rows_s = c.reshape(x.shape[seq_axis], pairs), s.reshape(x.shape[seq_axis], pairs)
+    else:
+        # one row for every position: the table is repeated along axis -2 (a copy of its rows)
+        seq_axis = x.ndim - 2 if x.ndim >= 2 else 0
+        n = x.shape[seq_axis] if x.ndim >= 2 else 1
+        rows_c = c.reshape(1, pairs).expand(n, pairs).contiguous()
+        rows_s = s.reshape(1, pairs).expand(n, pairs).contiguous()
+        if x.ndim == 1:
+            return _Rotate.apply(x.reshape(1, -1), rows_c, rows_s, 0).reshape(x.shape)
+    return _Rotate.apply(x, rows_c, rows_s, seq_axis)
+
+
 def apply_ago_rotations(q, k, rotary_params=None, seq_axis=None):
     """Apply AGO Cayley rotations to q and k (src/attention.py:207-240); returns (q_rot, k_rot)
     in the input dtypes."""

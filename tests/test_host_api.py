@@ -122,6 +122,30 @@ def test_apply_ago_rotations_checks():
         A.apply_ago_rotations(q, q, rotary_params=3.0)
 
 
+def test_align_param_and_rotate_tensor_checks():
+    """_align_param (src/attention.py:123-139) is a view of the table's first seq_len rows shaped
+    to broadcast on the sequence axis, which it infers as the reference does; _rotate_tensor
+    (:142-152) refuses tables that do not broadcast against the feature pairs and, on host
+    tensors, fails loudly like every other entry point."""
+    from algebraic_intelligence_amd.attention import _align_param, _rotate_tensor
+    c = torch.arange(32 * 4, dtype=torch.float32).reshape(32, 4)
+    a = _align_param(c, (2, 3, 16, 8), seq_axis=2)
+    assert a.shape == (1, 1, 16, 4) and torch.equal(a[0, 0], c[:16]) and a.data_ptr() == c.data_ptr()
+    assert _align_param(c, (2, 16, 3, 8)).shape == (1, 16, 1, 4)  # (B, T, H, D): T > H, T <= rows
+    assert _align_param(c, (2, 3, 16, 8)).shape == (1, 1, 16, 4)
+    assert _align_param(c, (2, 16, 8)).shape == (1, 16, 4)
+    assert _align_param(c, (16, 8)).shape == (16, 4)
+    x = torch.zeros(2, 3, 16, 8)
+    with pytest.raises(ValueError, match="even"):
+        _rotate_tensor(torch.zeros(2, 3, 16, 7), a, a)
+    with pytest.raises(ValueError, match="broadcast"):
+        _rotate_tensor(x, c[:16, :3], c[:16, :3])
+    with pytest.raises(ValueError, match="one axis"):
+        _rotate_tensor(x, torch.zeros(1, 3, 16, 4), torch.zeros(1, 3, 16, 4))
+    with pytest.raises(RuntimeError, match="GPU"):
+        _rotate_tensor(x, a, a)
+
+
 def test_flop_count_matches_definition():
     # 4 B H D N_pairs; non-causal is the reference's 4 b h l^2 d (scripts/run_phase6_tpu.py:236)
     assert A.afa_flops(8, 12, 4096, 64, True) == 4 * 8 * 12 * 64 * 4096 * 4097 // 2
