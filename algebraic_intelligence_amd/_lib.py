@@ -42,6 +42,7 @@ SIGNATURES = {
     "asoftmax_fwd": (_int, [_int, _i64, _i64, _vp, _vp, _dbl, _dbl, _vp]),
     "asoftmax_bwd": (_int, [_int, _i64, _i64, _vp, _vp, _vp, _dbl, _dbl, _vp]),
     "octic_fwd": (_int, [_int, _i64, _vp, _vp, _vp]),
+    "octic_fwd_r": (_int, [_int, _i64, _vp, _vp, _vp, _vp]),
     "octic_bwd": (_int, [_int, _i64, _vp, _vp, _vp, _vp]),
     "ago_build_tables": (_int, [_int, _i64, _i64, _vp, _dbl, _vp, _vp, _vp]),
     "ago_rotate": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _vp, _vp, _i64, _vp]),

@@ -68,6 +68,29 @@ def _vmu_octic_kernel(s: torch.Tensor) -> torch.Tensor:
     return octic_kernel(s)
 
 
+# the differentiable octic weight under the reference's private name (src/attention.py:34-44)
+_octic = octic_kernel
+
+
+def _kernel(z):
+    """(rho(z)^8, r) with r = rsqrt(1 + z^2), from one evaluation (src/attention.py:18-26): the
+    octic weight and the factor of its VJP 8 r rho^8 g.  Both come back in the accumulation type,
+    fp32 (fp64 for fp64 z), which is the type the reference's callers hand it (_accumulate,
+    src/primitives.py:17-21).  Not differentiable, as in the reference, whose custom VJPs use r
+    instead."""
+    z = _float_input(z)
+    dev = _lib.require_device(z)
+    zc = z.contiguous()
+    acc = _lib.accum_dtype(z.dtype)
+    k = torch.empty(zc.shape, dtype=acc, device=dev)
+    r = torch.empty(zc.shape, dtype=acc, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().octic_fwd_r(_lib.dtype_code(z.dtype), zc.numel(), _lib.ptr(zc), _lib.ptr(k), _lib.ptr(r),
+                                    _lib.stream_ptr(dev))
+    _lib.check(rc, "octic_fwd_r")
+    return k, r
+
+
 # ------------------------------------------------------------------------------ A-Softmax
 class _ASoftmax(torch.autograd.Function):
     @staticmethod

@@ -531,6 +531,14 @@ int octic_fwd(int dtype, int64_t n, const void* x, void* y, void* stream) {
   return hip_status(afa::octic_fwd_launch(dtype, n, x, y, (hipStream_t)stream));
 }
 
+int octic_fwd_r(int dtype, int64_t n, const void* x, void* k, void* r, void* stream) {
+  if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
+  if (!x || !k || !r) return AFA_ERR_NULL;
+  if (n < 0) return AFA_ERR_SHAPE;
+  if (n == 0) return AFA_OK;
+  return hip_status(afa::octic_fwd_r_launch(dtype, n, x, k, r, (hipStream_t)stream));
+}
+
 int octic_bwd(int dtype, int64_t n, const void* x, const void* g, void* dx, void* stream) {
   if (!valid_dtype(dtype)) return AFA_ERR_DTYPE;
   if (!x || !g || !dx) return AFA_ERR_NULL;

@@ -161,6 +161,7 @@ hipError_t asoftmax_fwd_launch(int dtype, int64_t rows, int64_t n, const void* x
 hipError_t asoftmax_bwd_launch(int dtype, int64_t rows, int64_t n, const void* x, const void* g,
                                void* dx, double sink, double eps, hipStream_t st);
 hipError_t octic_fwd_launch(int dtype, int64_t n, const void* x, void* y, hipStream_t st);
+hipError_t octic_fwd_r_launch(int dtype, int64_t n, const void* x, void* k, void* r, hipStream_t st);
 
 // Final division of a ring's accumulators (afa_generic.hip); strides in elements.
 struct RingFinish {

@@ -165,6 +165,19 @@ __global__ __launch_bounds__(256) void octic_fwd_kernel(int64_t n, const void* x
   sstore<DT>(y, i, octic_ref(sload<DT>(x, i), r));
 }
 
+// rho(x)^8 and r = rsqrt(1 + x^2), both stored in the accumulation type (fp32, fp64 for fp64
+// inputs): src/attention.py:18-26 returns the pair, r being the factor of the VJP 8 r rho^8 g.
+template <int DT>
+__global__ __launch_bounds__(256) void octic_fwd_r_kernel(int64_t n, const void* x, void* k, void* r) {
+  typedef typename SAcc<DT>::T T;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  T rr;
+  const T kk = octic_ref(sload<DT>(x, i), rr);
+  ((T*)k)[i] = kk;
+  ((T*)r)[i] = rr;
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void octic_bwd_kernel(int64_t n, const void* x, const void* g,
                                                         void* dx) {
@@ -418,6 +431,10 @@ static void oc_fwd(int64_t n, const void* x, void* y, hipStream_t st) {
   hipLaunchKernelGGL((octic_fwd_kernel<DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, n, x, y);
 }
 template <int DT>
+static void oc_fwd_r(int64_t n, const void* x, void* k, void* r, hipStream_t st) {
+  hipLaunchKernelGGL((octic_fwd_r_kernel<DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, n, x, k, r);
+}
+template <int DT>
 static void oc_bwd(int64_t n, const void* x, const void* g, void* dx, hipStream_t st) {
   hipLaunchKernelGGL((octic_bwd_kernel<DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, n, x, g, dx);
 }
@@ -476,6 +493,10 @@ hipError_t asoftmax_bwd_launch(int dtype, int64_t rows, int64_t n, const void* x
 }
 hipError_t octic_fwd_launch(int dtype, int64_t n, const void* x, void* y, hipStream_t st) {
   AFA_DISPATCH_DT(dtype, oc_fwd, n, x, y, st);
+  return hipGetLastError();
+}
+hipError_t octic_fwd_r_launch(int dtype, int64_t n, const void* x, void* k, void* r, hipStream_t st) {
+  AFA_DISPATCH_DT(dtype, oc_fwd_r, n, x, k, r, st);
   return hipGetLastError();
 }
 hipError_t octic_bwd_launch(int dtype, int64_t n, const void* x, const void* g, void* dx, hipStream_t st) {

@@ -169,6 +169,10 @@ int asoftmax_bwd(int dtype, int64_t rows, int64_t cols, const void* x, const voi
  * (src/attention.py:18-50, src/kernels/pallas_afa.py:32-49). */
 int octic_fwd(int dtype, int64_t n, const void* x, void* y, void* stream);
 int octic_bwd(int dtype, int64_t n, const void* x, const void* g, void* dx, void* stream);
+/* rho(x)^8 and r = rsqrt(1 + x^2) in the same evaluation, both written in the accumulation type
+ * (fp32, or fp64 for AFA_F64 inputs).  Replaces _kernel (src/attention.py:18-26), which returns
+ * the pair: r is the factor of the VJP 8 r rho^8 g. */
+int octic_fwd_r(int dtype, int64_t n, const void* x, void* k, void* r, void* stream);
 
 /*
  * Cayley rotary tables.  Replaces build_cayley_rotary_matrix (src/attention.py:155-204):

@@ -188,6 +188,10 @@ def test_asoftmax_octic_ago_reject_invalid_arguments(lib):
     assert lib.asoftmax_bwd(_lib.AFA_F32, 4, 8, DUMMY, None, DUMMY, 0.5, 1e-5, None) == _lib.ERR_NULL
     assert lib.octic_fwd(11, 4, DUMMY, DUMMY, None) == _lib.ERR_DTYPE
     assert lib.octic_bwd(_lib.AFA_F32, -1, DUMMY, DUMMY, DUMMY, None) == _lib.ERR_SHAPE
+    assert lib.octic_fwd_r(11, 4, DUMMY, DUMMY, DUMMY, None) == _lib.ERR_DTYPE
+    assert lib.octic_fwd_r(_lib.AFA_F32, 4, DUMMY, DUMMY, None, None) == _lib.ERR_NULL
+    assert lib.octic_fwd_r(_lib.AFA_F32, -1, DUMMY, DUMMY, DUMMY, None) == _lib.ERR_SHAPE
+    assert lib.octic_fwd_r(_lib.AFA_F32, 0, DUMMY, DUMMY, DUMMY, None) == _lib.OK
     assert lib.ago_build_tables(_lib.AFA_BF16, 8, 16, None, 1e4, DUMMY, DUMMY, None) == _lib.ERR_DTYPE
     assert lib.ago_build_tables(_lib.AFA_F32, 7, 16, None, 1e4, DUMMY, DUMMY, None) == _lib.ERR_SHAPE
     assert lib.ago_rotate(_lib.AFA_F32, 1, 16, 1, 8, DUMMY, DUMMY, _lib.AFA_F32, DUMMY, DUMMY, 15,

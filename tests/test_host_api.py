@@ -146,6 +146,16 @@ def test_align_param_and_rotate_tensor_checks():
         _rotate_tensor(x, a, a)
 
 
+def test_octic_pair_checks():
+    """_kernel (src/attention.py:18-26) takes floating point input only and runs on the GPU."""
+    from algebraic_intelligence_amd.attention import _kernel, _octic
+    assert _octic is A.octic_kernel
+    with pytest.raises(TypeError):
+        _kernel(torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="GPU"):
+        _kernel(torch.zeros(4))
+
+
 def test_flop_count_matches_definition():
     # 4 B H D N_pairs; non-causal is the reference's 4 b h l^2 d (scripts/run_phase6_tpu.py:236)
     assert A.afa_flops(8, 12, 4096, 64, True) == 4 * 8 * 12 * 64 * 4096 * 4097 // 2

@@ -379,6 +379,36 @@ def test_octic_kernel_and_derivative(gold, dtype, tol):
     np.testing.assert_allclose(to_f64(dx), O.rho8_derivative(to_f64(x)), rtol=tol * 4)
 
 
+@pytest.mark.parametrize("dtype,tol,rtol", [(torch.float64, 1e-14, 1e-15), (torch.float32, 3e-6, 1e-6)])
+def test_octic_pair_with_r(gold, dtype, tol, rtol):
+    """_kernel returns (rho^8, r) from one evaluation (src/attention.py:18-26): rho^8 against the
+    40-digit fixtures and bitwise equal to octic_kernel, r against 1/sqrt(1 + x^2), and the known
+    answer rho(2)^8 = 51841 + 23184 sqrt(5), r(2) = 1/sqrt(5) (tests/test_attention.py:34)."""
+    from algebraic_intelligence_amd.attention import _kernel
+    x = _t(gold["rho8_x"], dtype)
+    k, r = _kernel(x)
+    assert k.dtype == dtype and r.dtype == dtype and k.shape == x.shape
+    np.testing.assert_allclose(to_f64(k), gold["rho8_y"], rtol=tol)
+    assert torch.equal(k, A.octic_kernel(x))
+    xf = to_f64(x)
+    np.testing.assert_allclose(to_f64(r), 1.0 / np.sqrt(1.0 + xf * xf), rtol=rtol)
+    k2, r2 = _kernel(torch.tensor([2.0, -2.0], dtype=dtype, device=DEV))
+    exact = 51841.0 + 23184.0 * np.sqrt(5.0)
+    np.testing.assert_allclose(to_f64(k2), [exact, 1.0 / exact], rtol=tol)
+    np.testing.assert_allclose(to_f64(r2), [1.0 / np.sqrt(5.0)] * 2, rtol=rtol)
+
+
+def test_octic_pair_promotes_16_bit_input():
+    """bf16 / fp16 input: the pair is evaluated and returned in fp32, as on the fp32 upcast."""
+    from algebraic_intelligence_amd.attention import _kernel
+    x = torch.linspace(-40, 40, 4001, device=DEV)
+    for dt in (torch.bfloat16, torch.float16):
+        xh = x.to(dt)
+        k, r = _kernel(xh)
+        kf, rf = _kernel(xh.float())
+        assert k.dtype == torch.float32 and torch.equal(k, kf) and torch.equal(r, rf)
+
+
 # ------------------------------------------------------------------------------ Cayley rotary
 def _f32_recurrence(w, L, base=10000.0, default=False):
     """The table recurrence with every operation rounded in float32, in the kernel's order."""
