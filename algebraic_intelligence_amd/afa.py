@@ -22,6 +22,7 @@ import torch
 
 from . import _lib
 from ._lib import table_2d
+from .attention import _vmu_octic_kernel  # noqa: F401  (src/kernels/pallas_afa.py:32-49 defines it here)
 
 __all__ = [
     "pallas_afa_forward", "tiled_afa_forward", "exact_afa_reference", "exact_afa_with_denominator",
@@ -87,6 +88,17 @@ def _launch_fwd(q, k, v, sink_omega, causal, valid_seq_len, rotary_params, flags
             _lib.ptr(ws), ws_bytes, _lib.stream_ptr(dev))
     _lib.check(rc, "afa_fwd")
     return out, den
+
+
+def afa_kernel(*refs, **config):
+    """The reference's tile body (src/kernels/pallas_afa.py:52-151) takes Pallas-TPU memory refs
+    and runs only inside pallas_call.  Here the tile loop is the HIP kernels of libafa_hip.so
+    (afa_fwd_d64_kernel, afa_fwd_pipe_kernel, afa_fwd_mfma_kernel, afa_fwd_f32_kernel), which
+    pallas_afa_forward launches; this name lets modules that import it load, and calling it
+    raises."""
+    raise NotImplementedError(
+        "afa_kernel is the Pallas-TPU tile body; on MI355X the tile loop runs inside libafa_hip.so: "
+        "call pallas_afa_forward (or tiled_afa_forward) with the whole q, k, v")
 
 
 def pallas_afa_forward(

@@ -156,6 +156,19 @@ def test_octic_pair_checks():
         _kernel(torch.zeros(4))
 
 
+def test_reference_module_names_import():
+    """Every name the reference's tests and scripts import from src/kernels/pallas_afa.py
+    (tests/test_pallas_afa.py:24-35, src/kernels/__init__.py:3-14) exists in afa.py; the Pallas
+    tile body afa_kernel raises when called (its loop runs inside the library)."""
+    from algebraic_intelligence_amd import afa as M
+    for n in ("_vmu_octic_kernel", "afa_kernel", "algebraic_flash_attention", "distributed_ring_afa",
+              "exact_afa_reference", "exact_afa_with_denominator", "pallas_afa", "pallas_afa_forward",
+              "sharded_pallas_afa", "tiled_afa_backward", "tiled_afa_forward"):
+        assert hasattr(M, n), n
+    with pytest.raises(NotImplementedError, match="pallas_afa_forward"):
+        M.afa_kernel(None, None, None, None, None, None, None, scale=0.125, sink_omega=0.5)
+
+
 def test_flop_count_matches_definition():
     # 4 B H D N_pairs; non-causal is the reference's 4 b h l^2 d (scripts/run_phase6_tpu.py:236)
     assert A.afa_flops(8, 12, 4096, 64, True) == 4 * 8 * 12 * 64 * 4096 * 4097 // 2
